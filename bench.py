@@ -1,0 +1,205 @@
+"""Batch-1 bf16 Qwen3-0.6B decode benchmark on one MI355X (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Workload: Qwen3-0.6B architecture (28 layers, hidden 1024, 16/8 heads x 128, MLP 3072, vocab
+151936, tied LM head), seeded N(0, 0.02) bf16 weights (megaqwen_amd.synthetic, seed 0), batch 1,
+greedy decode.  A step is one decoded token (one persistent decode kernel launch).  Exactly K
+steps are timed at each position bucket: positions 1..K, 128..127+K (the headline `value`) and
+4096..4095+K; the KV cache is filled to the bucket start with untimed decode steps.  Inputs are
+resident in HBM; the timed region is a device-side token chain (no host round trip per token).
+
+Roofline: algorithmic bytes per token = bf16 weights streamed (1,192,101,888 B) + KV read
+(114,688 B x (pos + 1)) + KV write (114,688 B), over the per-launch duration measured with HIP
+events on the launch stream, against 8 TB/s.
+
+cpu_baseline: the CPU oracle (oracle/ref_cpu.py, PyTorch fp32 restatement of the reference decode
+path) on BASELINE config 1 (16-token prompt fed through decode, then 32 greedy tokens), timed on
+this host with all its cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12
+WEIGHT_BYTES = 1_192_101_888
+KV_BYTES_PER_POS = 28 * 8 * 128 * 2 * 2     # K + V, all layers, bf16
+
+
+def bytes_per_token(pos: int) -> int:
+    return WEIGHT_BYTES + KV_BYTES_PER_POS * (pos + 1) + KV_BYTES_PER_POS
+
+
+def build_decoder(max_seq: int):
+    import torch
+    from megaqwen_amd.decoder import MegakernelPrefillDecoder
+    from megaqwen_amd.rope import build_rope_tables
+    from megaqwen_amd.spec import _DEFAULT_MODEL_SPEC
+    from megaqwen_amd.synthetic import make_weights
+
+    spec = dict(_DEFAULT_MODEL_SPEC)
+    w = make_weights(spec, seed=0)
+    cos, sin = build_rope_tables(max_seq, 1e6, 128)
+    emb = w["embed_weight"].cuda()
+    layers = [t.cuda() for t in w["layer_weights"]]
+    dec = MegakernelPrefillDecoder(emb, layers, w["final_norm_weight"].cuda(), emb, cos.cuda(),
+                                   sin.cuda(), spec["num_layers"], max_seq, max_prefill_len=0)
+    return dec, spec
+
+
+def time_bucket(dec, start_pos: int, steps: int, first_token: int):
+    """Fills the cache to `start_pos`, then times `steps` decode launches one by one with event
+    pairs (per-launch duration) inside one region bracketed by synchronize (wall time)."""
+    import torch
+    dec.reset()
+    tok = first_token
+    if start_pos > 0:
+        toks = dec.decode_steps_cuda(tok, start_pos)
+        tok = int(toks[-1].item())
+    assert dec.position() == start_pos
+    buf = torch.empty(steps + 1, dtype=torch.int32, device="cuda")
+    buf[0] = tok
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    lib, h = dec._lib, dec._h
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        rc = lib.mq_decode_steps(h, buf.data_ptr() + 4 * i, 1, sp)
+        ev[i][1].record(stream)
+        if rc != 0:
+            raise RuntimeError(lib.mq_last_error().decode())
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_launch = sum(a.elapsed_time(b) for a, b in ev) / steps / 1e3
+    dec.check()
+    return wall, per_launch
+
+
+def cpu_baseline(prompt_len: int = 16, gen: int = 32):
+    import torch
+    from megaqwen_amd.rope import build_rope_tables
+    from megaqwen_amd.spec import _DEFAULT_MODEL_SPEC
+    from megaqwen_amd.synthetic import make_tokens, make_weights
+    from oracle.ref_cpu import OracleModel
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    spec = dict(_DEFAULT_MODEL_SPEC)
+    w = make_weights(spec, seed=0, dtype=torch.float32)
+    cos, sin = build_rope_tables(prompt_len + gen + 2, 1e6, 128)
+    m = OracleModel(w, spec, cos, sin, prompt_len + gen + 2, round_bf16=True)
+    prompt = make_tokens(prompt_len, spec["vocab_size"], seed=0).tolist()
+    for t in prompt[:-1]:
+        m.decode_step(t, return_logits=False)
+    tok = m.decode_step(prompt[-1], return_logits=False)          # warm-up token
+    t0 = time.perf_counter()
+    for _ in range(gen):
+        tok = m.decode_step(tok, return_logits=False)
+    dt = time.perf_counter() - t0
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": gen / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"config 1: 28-layer fp32 CPU oracle, {prompt_len}-token prompt fed through "
+                      f"decode, {gen} greedy tokens timed ({dt:.1f} s); os.cpu_count()={threads}; "
+                      f"{cpu_model}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mode", default="persistent", choices=["persistent", "multi_kernel"])
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): this build has no "
+              "multi-GPU path; see the sharding note in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    K, W = int(args.steps), int(args.warmup)
+    positions = (1, 128, 4096)
+    max_seq = positions[-1] + K + 8
+    dec, spec = build_decoder(max_seq)
+    dec.set_mode(args.mode)
+    print(f"[bench] decoder ready: mode={dec.mode} grid={dec.grid} max_seq={max_seq}", file=sys.stderr,
+          flush=True)
+    first = 9707
+    # warm-up (untimed)
+    dec.reset()
+    dec.decode_steps_cuda(first, W)
+    torch.cuda.synchronize()
+    res = {}
+    for p in positions:
+        wall, per_launch = time_bucket(dec, p, K, first)
+        tok_s = K / wall
+        mid = p + (K - 1) / 2
+        res[p] = {"tok_s": tok_s, "ms_per_token": 1e3 * wall / K,
+                  "kernel_us": per_launch * 1e6,
+                  "bytes_per_token": bytes_per_token(int(mid)),
+                  "roofline_frac_wall": bytes_per_token(int(mid)) * tok_s / HBM_PEAK,
+                  "roofline_frac_kernel": bytes_per_token(int(mid)) / per_launch / HBM_PEAK}
+        print(f"[bench] pos {p}: {tok_s:.1f} tok/s, kernel {per_launch * 1e6:.1f} us, "
+              f"roofline {res[p]['roofline_frac_wall'] * 100:.1f}% (wall) "
+              f"{res[p]['roofline_frac_kernel'] * 100:.1f}% (kernel)", file=sys.stderr, flush=True)
+
+    head = res[128]
+    achieved = head["bytes_per_token"] / (head["kernel_us"] * 1e-6)
+    cpu = None
+    if not args.no_cpu_baseline:
+        del dec
+        torch.cuda.empty_cache()
+        cpu = cpu_baseline()
+        print(f"[bench] cpu baseline {cpu['value']:.2f} tok/s on {cpu['cores']} threads",
+              file=sys.stderr, flush=True)
+    line = {
+        "metric": "batch-1 decode tok/s at pos 1/128/4096 + % HBM roofline, Qwen3-0.6B bf16",
+        "value": round(head["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(head["ms_per_token"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) random-init weights, greedy token chain)",
+        "config": {"workload": "Qwen3-0.6B-architecture batch-1 greedy decode; value = positions "
+                               f"128..{127 + K}", "layers": 28, "hidden": 1024, "vocab": 151936,
+                   "kv_heads": 8, "head_dim": 128, "decode_mode": args.mode,
+                   "tok_s_by_position": {str(p): round(r["tok_s"], 2) for p, r in res.items()},
+                   "roofline_frac_by_position": {str(p): round(r["roofline_frac_wall"], 4)
+                                                 for p, r in res.items()}},
+        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 2), "peak": 8000.0,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "kernel": "mq_decode_persistent_kernel" if args.mode == "persistent"
+                     else "mq_decode_phase_kernel (all phases)",
+                     "kernel_us": round(head["kernel_us"], 2),
+                     "bytes_per_launch": head["bytes_per_token"]},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

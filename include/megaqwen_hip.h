@@ -1,0 +1,170 @@
+/* megaqwen_hip.h — C ABI of libmegaqwen_hip.so, the MI355X (gfx950) batch-1 Qwen3-0.6B
+ * decode / prefill library.
+ *
+ * Plain C: device pointers are `void*` / typed pointers to device memory, streams are the
+ * `hipStream_t` value passed as `void*` (NULL = default stream).  Every function returns
+ * MQ_OK (0) or a negative MQ_ERR_* code; mq_last_error() describes the last failure of the
+ * calling thread.  No function takes ownership of caller memory.
+ *
+ * Reference interfaces replaced (baicai-1145/MegaQwen, paths relative to its root):
+ *   struct LDGLayerWeights ............ csrc/megakernel/fused_decode_ldg_common.inl:97-109
+ *   MegakernelDecoder (ctor, decode_step, reset, position)
+ *                                       csrc/megakernel/bindings_decode.cpp:80-280
+ *   launch_ldg_decode / launch_ldg_decode_with_logits
+ *                                       csrc/megakernel/fused_decode_ldg_launch.inl:55-364
+ *   MegakernelPrefillDecoder.prefill_step / decode_steps_cuda
+ *                                       csrc/megakernel/bindings_prefill.cpp:731-833,1045-1075
+ *   launch_prefill_float .............. csrc/megakernel/fused_prefill_launch.inl:71-731
+ */
+#ifndef MEGAQWEN_HIP_H
+#define MEGAQWEN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MQ_ABI_VERSION 1
+
+#define MQ_OK 0
+#define MQ_ERR_INVALID_ARG -1     /* null pointer, bad size, unsupported shape */
+#define MQ_ERR_HIP -2             /* a HIP runtime call failed */
+#define MQ_ERR_POSITION -3        /* position would exceed max_seq_len */
+#define MQ_ERR_DEVICE -4          /* the kernel reported an error (barrier time-out, bad input) */
+#define MQ_ERR_UNSUPPORTED -5     /* e.g. cooperative launch not available for persistent mode */
+
+/* Decode kernel organisation. */
+#define MQ_MODE_PERSISTENT 0      /* one cooperative kernel per token, grid barriers between phases */
+#define MQ_MODE_MULTI_KERNEL 1    /* one kernel launch per phase (no grid barriers) */
+
+/* One layer's bf16 weights (row-major, contiguous), same order and meaning as the reference's
+ * LDGLayerWeights (fused_decode_ldg_common.inl:97-109) and its 11-per-layer flat list
+ * (megakernel_weights.py:109-128). */
+typedef struct mq_layer_weights {
+  const void* input_layernorm;     /* [H]            */
+  const void* q_proj;              /* [Hq*D, H]      */
+  const void* k_proj;              /* [Hkv*D, H]     */
+  const void* v_proj;              /* [Hkv*D, H]     */
+  const void* q_norm;              /* [D]            */
+  const void* k_norm;              /* [D]            */
+  const void* o_proj;              /* [H, Hq*D]      */
+  const void* post_attn_layernorm; /* [H]            */
+  const void* gate_proj;           /* [I, H]         */
+  const void* up_proj;             /* [I, H]         */
+  const void* down_proj;           /* [H, I]         */
+} mq_layer_weights;
+
+/* Model description: the constructor arguments of MegakernelDecoder /
+ * MegakernelPrefillDecoder (bindings_decode.cpp:82-191, bindings_prefill.cpp:1639-1674). */
+typedef struct mq_model_desc {
+  int hidden_size;        /* must be 1024 (compiled layer shape) */
+  int intermediate_size;  /* 3072 */
+  int num_q_heads;        /* 16 */
+  int num_kv_heads;       /* 8 */
+  int head_dim;           /* 128 */
+  int num_layers;         /* >= 1 */
+  int vocab_size;         /* >= 1 */
+  int max_seq_len;        /* KV-cache capacity in positions */
+  int max_prefill_len;    /* 0 = decode only */
+  const void* embed;      /* bf16 [vocab, H] */
+  const void* final_norm; /* bf16 [H] */
+  const void* lm_head;    /* bf16 [vocab, H] (may equal embed: tied) */
+  const void* cos_table;  /* bf16 [max_seq_len, D] */
+  const void* sin_table;  /* bf16 [max_seq_len, D] */
+  const mq_layer_weights* layers; /* host array [num_layers] of device pointers */
+} mq_model_desc;
+
+typedef struct mq_decoder mq_decoder;
+
+int mq_abi_version(void);
+const char* mq_last_error(void);
+
+/* Bytes of the zero-initialised device workspace a decoder needs (sync state, layer table,
+ * activations, attention partials and, when max_prefill_len > 0, prefill buffers). */
+size_t mq_workspace_bytes(const mq_model_desc* desc);
+
+/* Bytes of ONE of the two KV caches: num_layers * num_kv_heads * max_seq_len * head_dim * 2.
+ * Layout [num_layers][num_kv_heads][max_seq_len][head_dim] bf16, as the reference
+ * (bindings_decode.cpp:127-130). */
+size_t mq_kv_cache_bytes(const mq_model_desc* desc);
+
+/* MegakernelDecoder(...) constructor.  k_cache, v_cache and workspace are caller-owned device
+ * buffers of the sizes above; the workspace must be zero-filled.  Position starts at 0. */
+int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, void* workspace,
+                      size_t workspace_bytes, mq_decoder** out);
+int mq_decoder_destroy(mq_decoder* dec);
+
+/* reset(): zeroes both KV caches and sets the position to 0 (bindings_decode.cpp:236-240). */
+int mq_decoder_reset(mq_decoder* dec, void* stream);
+/* position() (bindings_decode.cpp:273-280).  Returns the host-side position counter. */
+int mq_decoder_position(const mq_decoder* dec);
+/* Sets the host-side position counter only (0 <= pos <= max_seq_len).  For callers that replay
+ * captured mq_decode_steps launches: the device-side position advances inside the kernels, the
+ * host counter (used for bounds checks and position()) does not. */
+int mq_decoder_set_host_position(mq_decoder* dec, int pos);
+/* Selects MQ_MODE_PERSISTENT or MQ_MODE_MULTI_KERNEL; returns MQ_ERR_UNSUPPORTED if the device
+ * cannot co-schedule the persistent grid. */
+int mq_decoder_set_mode(mq_decoder* dec, int mode);
+int mq_decoder_get_mode(const mq_decoder* dec);
+/* Workgroups per decode launch (one per compute unit). */
+int mq_decoder_grid(const mq_decoder* dec);
+
+/* One decode step (launch_ldg_decode / launch_ldg_decode_with_logits): consumes the token at
+ * d_token_in, writes the greedy next token to d_token_out and, if d_logits is non-NULL, the
+ * fp32 logits [vocab].  Asynchronous on `stream`; advances the position by one.  Fails with
+ * MQ_ERR_POSITION when position >= max_seq_len. */
+int mq_decode_step(mq_decoder* dec, const int32_t* d_token_in, int32_t* d_token_out,
+                   float* d_logits, void* stream);
+
+/* decode_steps_cuda (bindings_prefill.cpp:1045-1075): d_tokens[0] holds the first token;
+ * step i reads d_tokens[i] and writes d_tokens[i+1], i < n.  The chain stays on the device. */
+int mq_decode_steps(mq_decoder* dec, int32_t* d_tokens, int n, void* stream);
+
+/* Debug hook (the reference's counterpart is debug_ldg_decode_cycles,
+ * bindings_prefill.cpp:980-1043): mq_decode_step that also writes the hidden state after every
+ * layer (bf16-rounded values as fp32) to d_hidden_trace [num_layers][hidden_size]. */
+int mq_debug_decode_step_layers(mq_decoder* dec, const int32_t* d_token_in,
+                                int32_t* d_token_out, float* d_logits, float* d_hidden_trace,
+                                void* stream);
+
+/* Debug hook, the counterpart of debug_ldg_decode_cycles (bindings_prefill.cpp:980-1043) and
+ * its per-block stage clock (fused_decode_ldg_common.inl:15-69): one persistent-mode decode step
+ * that records 100 MHz timestamps to d_stamps [grid][num_layers][11]: per layer, the start, then
+ * for each of the 5 phases "compute done" and "barrier passed". */
+int mq_debug_decode_step_timing(mq_decoder* dec, const int32_t* d_token_in,
+                                int32_t* d_token_out, uint64_t* d_stamps, void* stream);
+
+/* Synchronises `stream` and returns MQ_ERR_DEVICE if a kernel flagged an error. */
+int mq_decoder_check(mq_decoder* dec, void* stream);
+
+/* prefill_step (bindings_prefill.cpp:731-833) over launch_prefill_float
+ * (fused_prefill_launch.inl:71-731): runs tokens d_tokens[0..n) at positions 0..n-1, fills the
+ * KV cache, writes the greedy next token to d_token_out (and the last position's fp32 logits to
+ * d_logits if non-NULL) and sets the position to n.  1 <= n <= max_prefill_len. */
+int mq_prefill(mq_decoder* dec, const int32_t* d_tokens, int n, int32_t* d_token_out,
+               float* d_logits, void* stream);
+
+/* ---- op-level entry points (per-op microbenchmarks; layer `layer` of the decoder's model) ----
+ * (a) RMSNorm + q|k|v GEMV + q/k RMSNorm + RoPE at `pos`; writes rotated q (fp32 [Hq*D]) and the
+ *     K/V cache rows at `pos` (fused_decode_ldg_common.inl:131-394). */
+int mq_op_qkv_rope(mq_decoder* dec, int layer, const void* d_x_bf16, int pos, float* d_q_out,
+                   void* stream);
+/* (b) GQA attention of rotated queries (fp32 [Hq*D]) over cache rows [0, cache_len) of `layer`
+ *     -> fp32 [Hq*D] (fused_decode_ldg_common.inl:417-794). */
+int mq_op_attention(mq_decoder* dec, int layer, const float* d_q, int cache_len, float* d_out,
+                    void* stream);
+/* (c) x_out = bf16(W_down(silu(W_gate n) * W_up n) + a), n = RMSNorm(a) * post_ln
+ *     (fused_decode_ldg_mlp.inl:70-217).  a: fp32 [H]. */
+int mq_op_mlp(mq_decoder* dec, int layer, const float* d_a, void* d_x_out_bf16, void* stream);
+/* (d) final RMSNorm + LM head + argmax of a bf16 hidden state (fused_decode_ldg_lm.inl:6-163);
+ *     d_logits may be NULL. */
+int mq_op_lm_head(mq_decoder* dec, const void* d_x_bf16, int32_t* d_token_out, float* d_logits,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEGAQWEN_HIP_H */

@@ -1,0 +1,374 @@
+// C ABI of libmegaqwen_hip.so (declared in include/megaqwen_hip.h).
+//
+// The decoder handle is a small host object: it owns no device memory.  KV caches and the
+// workspace (sync state, device layer-pointer table, activations, attention partials, prefill
+// buffers) are caller-owned, so a Python caller can keep them as torch tensors, as the
+// reference's chat.py keeps its caches (chat.py:409-421).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+#include <string>
+
+#include "../../include/megaqwen_hip.h"
+#include "mq_decode.h"
+#include "mq_prefill.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct Layout {
+  size_t state, layers, scratch, prefill, total;
+};
+
+Layout layout_of(const mq_model_desc* d) {
+  Layout L;
+  L.state = 0;
+  L.layers = align_up(L.state + sizeof(MqState), 256);
+  L.scratch = align_up(L.layers + sizeof(MqLayerW) * (size_t)d->num_layers, 256);
+  L.prefill = align_up(L.scratch + sizeof(MqScratch), 256);
+  L.total = align_up(L.prefill + mq_prefill_workspace_bytes(d->max_prefill_len), 256);
+  return L;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_desc(const mq_model_desc* d) {
+  if (d == nullptr) return fail(MQ_ERR_INVALID_ARG, "model description is NULL");
+  if (d->hidden_size != MQ_H || d->intermediate_size != MQ_I || d->num_q_heads != MQ_NQ ||
+      d->num_kv_heads != MQ_NKV || d->head_dim != MQ_D)
+    return fail(MQ_ERR_INVALID_ARG,
+                "layer shape (hidden %d, intermediate %d, heads %d/%d, head_dim %d) differs from "
+                "the compiled Qwen3-0.6B shape (1024, 3072, 16/8, 128)",
+                d->hidden_size, d->intermediate_size, d->num_q_heads, d->num_kv_heads,
+                d->head_dim);
+  if (d->num_layers < 1 || d->num_layers > 4096)
+    return fail(MQ_ERR_INVALID_ARG, "num_layers %d out of range", d->num_layers);
+  if (d->vocab_size < 1) return fail(MQ_ERR_INVALID_ARG, "vocab_size %d < 1", d->vocab_size);
+  if (d->max_seq_len < 1) return fail(MQ_ERR_INVALID_ARG, "max_seq_len %d < 1", d->max_seq_len);
+  if (d->max_prefill_len < 0 || d->max_prefill_len > d->max_seq_len)
+    return fail(MQ_ERR_INVALID_ARG, "max_prefill_len %d must be in [0, max_seq_len=%d]",
+                d->max_prefill_len, d->max_seq_len);
+  const void* top[] = {d->embed, d->final_norm, d->lm_head, d->cos_table, d->sin_table};
+  for (const void* t : top)
+    if (t == nullptr || !aligned16(t))
+      return fail(MQ_ERR_INVALID_ARG, "model tensors must be non-NULL and 16-byte aligned");
+  if (d->layers == nullptr) return fail(MQ_ERR_INVALID_ARG, "layers array is NULL");
+  for (int l = 0; l < d->num_layers; ++l) {
+    const void* const* f = reinterpret_cast<const void* const*>(&d->layers[l]);
+    for (int i = 0; i < 11; ++i)
+      if (f[i] == nullptr || !aligned16(f[i]))
+        return fail(MQ_ERR_INVALID_ARG,
+                    "layer %d weight %d is NULL or not 16-byte aligned", l, i);
+  }
+  return MQ_OK;
+}
+
+}  // namespace
+
+struct mq_decoder {
+  MqDecodeParams p;
+  Layout lay;
+  int mode;
+  int grid;
+  int pos;
+  int max_prefill;
+  size_t kv_bytes;
+  char* ws;
+  MqPrefillBuffers pf;
+};
+
+extern "C" {
+
+int mq_abi_version(void) { return MQ_ABI_VERSION; }
+
+const char* mq_last_error(void) { return g_err.c_str(); }
+
+size_t mq_workspace_bytes(const mq_model_desc* desc) {
+  if (check_desc(desc) != MQ_OK) return 0;
+  return layout_of(desc).total;
+}
+
+size_t mq_kv_cache_bytes(const mq_model_desc* desc) {
+  if (check_desc(desc) != MQ_OK) return 0;
+  return (size_t)desc->num_layers * MQ_NKV * (size_t)desc->max_seq_len * MQ_D * sizeof(bf16_t);
+}
+
+int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, void* workspace,
+                      size_t workspace_bytes, mq_decoder** out) {
+  if (out == nullptr) return fail(MQ_ERR_INVALID_ARG, "out is NULL");
+  *out = nullptr;
+  int rc = check_desc(desc);
+  if (rc != MQ_OK) return rc;
+  const Layout lay = layout_of(desc);
+  if (workspace == nullptr || workspace_bytes < lay.total || (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return fail(MQ_ERR_INVALID_ARG, "workspace must be 256-byte aligned and >= %zu bytes",
+                lay.total);
+  if (k_cache == nullptr || v_cache == nullptr || !aligned16(k_cache) || !aligned16(v_cache))
+    return fail(MQ_ERR_INVALID_ARG, "KV caches must be non-NULL and 16-byte aligned");
+
+  int grid = 0, mode = MQ_MODE_PERSISTENT;
+  if (mq_decode_grid(MQ_MODE_PERSISTENT, &grid) != 0) {
+    mode = MQ_MODE_MULTI_KERNEL;
+    if (mq_decode_grid(MQ_MODE_MULTI_KERNEL, &grid) != 0)
+      return fail(MQ_ERR_HIP, "cannot query the HIP device");
+  }
+  if (grid < 64)
+    return fail(MQ_ERR_UNSUPPORTED, "device has %d compute units; at least 64 are required",
+                grid);
+
+  char* ws = static_cast<char*>(workspace);
+  // Device copy of the layer-pointer table (LDGLayerWeights[] of bindings_decode.cpp:119-122).
+  MqLayerW* host_layers = new (std::nothrow) MqLayerW[desc->num_layers];
+  if (host_layers == nullptr) return fail(MQ_ERR_INVALID_ARG, "out of host memory");
+  for (int l = 0; l < desc->num_layers; ++l) {
+    const mq_layer_weights& s = desc->layers[l];
+    MqLayerW& d = host_layers[l];
+    d.in_ln = static_cast<const bf16_t*>(s.input_layernorm);
+    d.wq = static_cast<const bf16_t*>(s.q_proj);
+    d.wk = static_cast<const bf16_t*>(s.k_proj);
+    d.wv = static_cast<const bf16_t*>(s.v_proj);
+    d.q_norm = static_cast<const bf16_t*>(s.q_norm);
+    d.k_norm = static_cast<const bf16_t*>(s.k_norm);
+    d.wo = static_cast<const bf16_t*>(s.o_proj);
+    d.post_ln = static_cast<const bf16_t*>(s.post_attn_layernorm);
+    d.wg = static_cast<const bf16_t*>(s.gate_proj);
+    d.wu = static_cast<const bf16_t*>(s.up_proj);
+    d.wd = static_cast<const bf16_t*>(s.down_proj);
+  }
+  hipError_t e = hipMemcpy(ws + lay.layers, host_layers, sizeof(MqLayerW) * desc->num_layers,
+                           hipMemcpyHostToDevice);
+  delete[] host_layers;
+  if (e != hipSuccess) return fail(MQ_ERR_HIP, "hipMemcpy(layer table): %s", hipGetErrorString(e));
+
+  mq_decoder* dec = new (std::nothrow) mq_decoder();
+  if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "out of host memory");
+  MqDecodeParams& p = dec->p;
+  memset(&p, 0, sizeof(p));
+  p.layers = reinterpret_cast<const MqLayerW*>(ws + lay.layers);
+  p.num_layers = desc->num_layers;
+  p.vocab = desc->vocab_size;
+  p.max_seq = desc->max_seq_len;
+  p.embed = static_cast<const bf16_t*>(desc->embed);
+  p.final_norm = static_cast<const bf16_t*>(desc->final_norm);
+  p.lm_head = static_cast<const bf16_t*>(desc->lm_head);
+  p.cos = static_cast<const bf16_t*>(desc->cos_table);
+  p.sin = static_cast<const bf16_t*>(desc->sin_table);
+  p.kc = static_cast<bf16_t*>(k_cache);
+  p.vc = static_cast<bf16_t*>(v_cache);
+  p.s = reinterpret_cast<MqScratch*>(ws + lay.scratch);
+  p.st = reinterpret_cast<MqState*>(ws + lay.state);
+  p.scale_log2 = (float)(1.4426950408889634 / sqrt((double)MQ_D));
+  dec->lay = lay;
+  dec->mode = mode;
+  dec->grid = grid;
+  dec->pos = 0;
+  dec->max_prefill = desc->max_prefill_len;
+  dec->kv_bytes = (size_t)desc->num_layers * MQ_NKV * (size_t)desc->max_seq_len * MQ_D * 2;
+  dec->ws = ws;
+  mq_prefill_bind(&dec->pf, ws + lay.prefill, desc->max_prefill_len);
+  if (mq_launch_fill_state(p.st, 0, nullptr) != 0 || hipStreamSynchronize(nullptr) != hipSuccess) {
+    delete dec;
+    return fail(MQ_ERR_HIP, "state initialisation failed");
+  }
+  *out = dec;
+  return MQ_OK;
+}
+
+int mq_decoder_destroy(mq_decoder* dec) {
+  delete dec;
+  return MQ_OK;
+}
+
+int mq_decoder_reset(mq_decoder* dec, void* stream) {
+  if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "decoder is NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mq_launch_zero(dec->p.kc, dec->kv_bytes, s) != 0 ||
+      mq_launch_zero(dec->p.vc, dec->kv_bytes, s) != 0 || mq_launch_fill_state(dec->p.st, 0, s) != 0)
+    return fail(MQ_ERR_HIP, "reset kernels failed to launch");
+  dec->pos = 0;
+  return MQ_OK;
+}
+
+int mq_decoder_position(const mq_decoder* dec) { return dec ? dec->pos : -1; }
+
+int mq_decoder_set_host_position(mq_decoder* dec, int pos) {
+  if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "decoder is NULL");
+  if (pos < 0 || pos > dec->p.max_seq)
+    return fail(MQ_ERR_POSITION, "position %d outside [0, %d]", pos, dec->p.max_seq);
+  dec->pos = pos;
+  return MQ_OK;
+}
+
+int mq_decoder_set_mode(mq_decoder* dec, int mode) {
+  if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "decoder is NULL");
+  if (mode != MQ_MODE_PERSISTENT && mode != MQ_MODE_MULTI_KERNEL)
+    return fail(MQ_ERR_INVALID_ARG, "unknown mode %d", mode);
+  int grid = 0;
+  if (mq_decode_grid(mode, &grid) != 0)
+    return fail(MQ_ERR_UNSUPPORTED, "mode %d is not available on this device", mode);
+  dec->mode = mode;
+  dec->grid = grid;
+  return MQ_OK;
+}
+
+int mq_decoder_get_mode(const mq_decoder* dec) { return dec ? dec->mode : -1; }
+int mq_decoder_grid(const mq_decoder* dec) { return dec ? dec->grid : -1; }
+
+int mq_decode_step(mq_decoder* dec, const int32_t* d_token_in, int32_t* d_token_out,
+                   float* d_logits, void* stream) {
+  if (dec == nullptr || d_token_in == nullptr || d_token_out == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "decoder and token pointers must be non-NULL");
+  if (dec->pos >= dec->p.max_seq)
+    return fail(MQ_ERR_POSITION, "decode position %d reaches max_seq_len %d", dec->pos,
+                dec->p.max_seq);
+  MqDecodeParams p = dec->p;
+  p.tok_in = d_token_in;
+  p.tok_out = d_token_out;
+  p.logits = d_logits;
+  int rc = mq_launch_decode(p, dec->mode, dec->grid, static_cast<hipStream_t>(stream));
+  if (rc != 0) return fail(MQ_ERR_HIP, "decode launch failed (%d)", rc);
+  dec->pos += 1;
+  return MQ_OK;
+}
+
+int mq_debug_decode_step_layers(mq_decoder* dec, const int32_t* d_token_in,
+                                int32_t* d_token_out, float* d_logits, float* d_hidden_trace,
+                                void* stream) {
+  if (dec == nullptr || d_token_in == nullptr || d_token_out == nullptr ||
+      d_hidden_trace == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "decoder, token and trace pointers must be non-NULL");
+  if (dec->pos >= dec->p.max_seq)
+    return fail(MQ_ERR_POSITION, "decode position %d reaches max_seq_len %d", dec->pos,
+                dec->p.max_seq);
+  MqDecodeParams p = dec->p;
+  p.tok_in = d_token_in;
+  p.tok_out = d_token_out;
+  p.logits = d_logits;
+  p.trace = d_hidden_trace;
+  int rc = mq_launch_decode(p, dec->mode, dec->grid, static_cast<hipStream_t>(stream));
+  if (rc != 0) return fail(MQ_ERR_HIP, "decode launch failed (%d)", rc);
+  dec->pos += 1;
+  return MQ_OK;
+}
+
+int mq_debug_decode_step_timing(mq_decoder* dec, const int32_t* d_token_in,
+                                int32_t* d_token_out, uint64_t* d_stamps, void* stream) {
+  if (dec == nullptr || d_token_in == nullptr || d_token_out == nullptr || d_stamps == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "decoder, token and stamp pointers must be non-NULL");
+  if (dec->mode != MQ_MODE_PERSISTENT)
+    return fail(MQ_ERR_UNSUPPORTED, "stage timing needs the persistent mode");
+  if (dec->pos >= dec->p.max_seq)
+    return fail(MQ_ERR_POSITION, "decode position %d reaches max_seq_len %d", dec->pos,
+                dec->p.max_seq);
+  MqDecodeParams p = dec->p;
+  p.tok_in = d_token_in;
+  p.tok_out = d_token_out;
+  p.stamps = d_stamps;
+  int rc = mq_launch_decode(p, dec->mode, dec->grid, static_cast<hipStream_t>(stream));
+  if (rc != 0) return fail(MQ_ERR_HIP, "decode launch failed (%d)", rc);
+  dec->pos += 1;
+  return MQ_OK;
+}
+
+int mq_decode_steps(mq_decoder* dec, int32_t* d_tokens, int n, void* stream) {
+  if (dec == nullptr || d_tokens == nullptr || n < 0)
+    return fail(MQ_ERR_INVALID_ARG, "bad decode_steps arguments");
+  if ((long long)dec->pos + n > dec->p.max_seq)
+    return fail(MQ_ERR_POSITION, "decode_steps would exceed max_seq_len (%d + %d > %d)",
+                dec->pos, n, dec->p.max_seq);
+  for (int i = 0; i < n; ++i) {
+    MqDecodeParams p = dec->p;
+    p.tok_in = d_tokens + i;
+    p.tok_out = d_tokens + i + 1;
+    p.logits = nullptr;
+    int rc = mq_launch_decode(p, dec->mode, dec->grid, static_cast<hipStream_t>(stream));
+    if (rc != 0) return fail(MQ_ERR_HIP, "decode launch %d failed (%d)", i, rc);
+    dec->pos += 1;
+  }
+  return MQ_OK;
+}
+
+int mq_decoder_check(mq_decoder* dec, void* stream) {
+  if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "decoder is NULL");
+  uint32_t err = 0;
+  if (mq_read_error(dec->p.st, static_cast<hipStream_t>(stream), &err) != 0)
+    return fail(MQ_ERR_HIP, "error-flag readback failed");
+  if (err != 0) return fail(MQ_ERR_DEVICE, "device error flag %u (1 = barrier time-out, 2 = bad position/token)", err);
+  return MQ_OK;
+}
+
+int mq_prefill(mq_decoder* dec, const int32_t* d_tokens, int n, int32_t* d_token_out,
+               float* d_logits, void* stream) {
+  if (dec == nullptr || d_tokens == nullptr || d_token_out == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "decoder and token pointers must be non-NULL");
+  if (n <= 0) return fail(MQ_ERR_INVALID_ARG, "Empty input sequence");
+  if (n > dec->max_prefill)
+    return fail(MQ_ERR_INVALID_ARG, "Prefill sequence length %d exceeds maximum %d", n,
+                dec->max_prefill);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = mq_launch_prefill(dec->p, dec->pf, d_tokens, n, d_token_out, d_logits, dec->grid, s);
+  if (rc != 0) return fail(MQ_ERR_HIP, "prefill launch failed (%d)", rc);
+  if (mq_launch_fill_state(dec->p.st, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
+  dec->pos = n;
+  return MQ_OK;
+}
+
+int mq_op_qkv_rope(mq_decoder* dec, int layer, const void* d_x_bf16, int pos, float* d_q_out,
+                   void* stream) {
+  if (dec == nullptr || d_x_bf16 == nullptr || d_q_out == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "NULL argument");
+  if (layer < 0 || layer >= dec->p.num_layers || pos < 0 || pos >= dec->p.max_seq)
+    return fail(MQ_ERR_INVALID_ARG, "layer %d / pos %d out of range", layer, pos);
+  int rc = mq_launch_op_qkv_rope(dec->p, layer, static_cast<const bf16_t*>(d_x_bf16), pos, d_q_out,
+                                 dec->grid, static_cast<hipStream_t>(stream));
+  return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%d)", rc);
+}
+
+int mq_op_attention(mq_decoder* dec, int layer, const float* d_q, int cache_len, float* d_out,
+                    void* stream) {
+  if (dec == nullptr || d_q == nullptr || d_out == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "NULL argument");
+  if (layer < 0 || layer >= dec->p.num_layers || cache_len < 1 || cache_len > dec->p.max_seq)
+    return fail(MQ_ERR_INVALID_ARG, "layer %d / cache_len %d out of range", layer, cache_len);
+  int rc = mq_launch_op_attention(dec->p, layer, d_q, cache_len, d_out, dec->grid,
+                                  static_cast<hipStream_t>(stream));
+  return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%d)", rc);
+}
+
+int mq_op_mlp(mq_decoder* dec, int layer, const float* d_a, void* d_x_out_bf16, void* stream) {
+  if (dec == nullptr || d_a == nullptr || d_x_out_bf16 == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "NULL argument");
+  if (layer < 0 || layer >= dec->p.num_layers)
+    return fail(MQ_ERR_INVALID_ARG, "layer %d out of range", layer);
+  int rc = mq_launch_op_mlp(dec->p, layer, d_a, static_cast<bf16_t*>(d_x_out_bf16), dec->grid,
+                            static_cast<hipStream_t>(stream));
+  return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%d)", rc);
+}
+
+int mq_op_lm_head(mq_decoder* dec, const void* d_x_bf16, int32_t* d_token_out, float* d_logits,
+                  void* stream) {
+  if (dec == nullptr || d_x_bf16 == nullptr || d_token_out == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "NULL argument");
+  int rc = mq_launch_op_lm_head(dec->p, static_cast<const bf16_t*>(d_x_bf16), d_token_out,
+                                d_logits, dec->grid, static_cast<hipStream_t>(stream));
+  return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%d)", rc);
+}
+
+}  // extern "C"

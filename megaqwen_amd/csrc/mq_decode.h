@@ -1,0 +1,110 @@
+// Shared host/device declarations of the decode path: device-side weight table, per-step
+// scratch, kernel parameters and the host launchers implemented in decode.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mq_config.h"
+#include "mq_device.h"
+
+// Device copy of one layer's weight pointers, in the order of the reference's LDGLayerWeights
+// (csrc/megakernel/fused_decode_ldg_common.inl:97-109) and of the public mq_layer_weights.
+struct MqLayerW {
+  const bf16_t* in_ln;
+  const bf16_t* wq;
+  const bf16_t* wk;
+  const bf16_t* wv;
+  const bf16_t* q_norm;
+  const bf16_t* k_norm;
+  const bf16_t* wo;
+  const bf16_t* post_ln;
+  const bf16_t* wg;
+  const bf16_t* wu;
+  const bf16_t* wd;
+};
+
+// fp32 activations of one decode step (lives in the caller's workspace).  Every array here is
+// written and read across workgroups with the coherent (sc1) accessors of mq_device.h.
+struct MqScratch {
+  float qkv[MQ_QKV];           // raw q | k | v projections (before q/k RMSNorm and RoPE)
+  float att[MQ_QDIM];          // merged attention output
+  float a[MQ_H];               // residual stream after attention: W_o att + x
+  float mlp[MQ_I];             // silu(gate) * up
+  float hidden[MQ_H];          // residual stream at a layer boundary: bf16-rounded values (the
+                               // reference keeps it in bf16, fused_decode_ldg_mlp.inl:200)
+  float part[MQ_NKV * MQ_MAX_CHUNKS * MQ_GQA * MQ_PART_STRIDE];  // attention split-K partials
+};
+
+struct MqState {
+  MqSync sync;
+  MqLine pos;                  // device-side decode position (read at step start, +1 at step end)
+};
+
+struct MqDecodeParams {
+  const MqLayerW* layers;      // device array [num_layers]
+  int num_layers;
+  int vocab;
+  int max_seq;
+  const bf16_t* embed;         // [vocab, H]
+  const bf16_t* final_norm;    // [H]
+  const bf16_t* lm_head;       // [vocab, H] (tied to embed for Qwen3-0.6B)
+  const bf16_t* cos;           // [max_seq, D] bf16
+  const bf16_t* sin;
+  bf16_t* kc;                  // [num_layers, NKV, max_seq, D]
+  bf16_t* vc;
+  const int* tok_in;           // device token id consumed by this step
+  int* tok_out;                // device argmax token written at the end of the step
+  float* logits;               // optional fp32 [vocab]
+  float* trace;                // optional fp32 [num_layers, H]: hidden state after every layer
+  uint64_t* stamps;            // optional [grid][num_layers][MQ_NSTAMP] 100 MHz timestamps
+  MqScratch* s;
+  MqState* st;
+  float scale_log2;            // log2(e) / sqrt(D): scores are kept in the log2 domain
+};
+
+// Per-layer timestamps of the persistent kernel's debug mode (s_memrealtime, 100 MHz):
+// 0 layer start, then for each of the 5 phases k: 2k+1 compute done (stores waited for),
+// 2k+2 barrier passed.
+#define MQ_NSTAMP 11
+
+// Attention work split: number of position chunks per kv head for a given cache length and
+// grid size, chosen so that every chunk is non-empty.  Shared by host and device.
+#define MQ_ATT_MIN_CHUNK MQ_ATT_BLOCK
+__host__ __device__ inline int mq_attn_nchunks(int cache_len, int grid) {
+  int maxc = grid / MQ_NKV;
+  if (maxc > MQ_MAX_CHUNKS) maxc = MQ_MAX_CHUNKS;
+  if (maxc < 1) maxc = 1;
+  int want = (cache_len + MQ_ATT_MIN_CHUNK - 1) / MQ_ATT_MIN_CHUNK;
+  if (want < 1) want = 1;
+  if (want > maxc) want = maxc;
+  int clen = (cache_len + want - 1) / want;
+  return (cache_len + clen - 1) / clen;
+}
+__host__ __device__ inline int mq_attn_chunk_len(int cache_len, int nch) {
+  return (cache_len + nch - 1) / nch;
+}
+
+// ---------------------------------------------------------------- host launchers (decode.hip)
+// Decode kernel organisation (values match MQ_MODE_* of include/megaqwen_hip.h).
+#ifndef MQ_MODE_PERSISTENT
+#define MQ_MODE_PERSISTENT 0
+#define MQ_MODE_MULTI_KERNEL 1
+#endif
+
+int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t stream);
+int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream);
+int mq_launch_zero(void* ptr, size_t bytes, hipStream_t stream);
+int mq_decode_grid(int mode, int* grid_out);
+int mq_read_error(MqState* st, hipStream_t stream, uint32_t* err_out);
+
+// op-level launchers (per-op microbenchmarks and parity tests)
+int mq_launch_op_qkv_rope(const MqDecodeParams& p, int layer, const bf16_t* x, int pos,
+                          float* q_out, int grid, hipStream_t stream);
+int mq_launch_op_attention(const MqDecodeParams& p, int layer, const float* q_hat, int cache_len,
+                           float* att_out, int grid, hipStream_t stream);
+int mq_launch_op_mlp(const MqDecodeParams& p, int layer, const float* a_in, bf16_t* x_out,
+                     int grid, hipStream_t stream);
+int mq_launch_op_lm_head(const MqDecodeParams& p, const bf16_t* x, int* tok_out, float* logits,
+                         int grid, hipStream_t stream);

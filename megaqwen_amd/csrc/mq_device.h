@@ -1,0 +1,232 @@
+// Device-side building blocks for the gfx950 (CDNA4) decode/prefill kernels.
+//
+// Everything here is written for wave64: reductions use DPP row operations inside a 16-lane
+// row and cross-row swizzles, never 32-lane warp shuffles.  bf16 values are carried as raw
+// 16-bit patterns (uint16_t) and widened with a shift, so no vendor bf16 type is involved.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mq_config.h"
+
+typedef uint16_t bf16_t;
+
+#define MQ_DEV __device__ __forceinline__
+
+// ---------------------------------------------------------------------------- bf16 <-> fp32
+MQ_DEV float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+MQ_DEV float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+MQ_DEV float bf16_to_f32(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (the rounding torch and __float2bfloat16 use).
+MQ_DEV bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)0x7fc0;  // NaN stays NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+MQ_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// ---------------------------------------------------------------------------- loads
+// Weights are streamed once per token and never fit in the 256 MB MALL next to the KV cache,
+// so they are loaded non-temporally (no L2 allocation priority).
+typedef unsigned int mq_u32x4 __attribute__((ext_vector_type(4)));
+MQ_DEV uint4 ld_nt16(const void* p) {
+  const mq_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const mq_u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+MQ_DEV uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// dot of 8 bf16 (one 16-byte load) with 8 fp32 values
+MQ_DEV float dot8(uint4 w, const float* x, float acc) {
+  acc = fmaf(bf16_lo(w.x), x[0], acc);
+  acc = fmaf(bf16_hi(w.x), x[1], acc);
+  acc = fmaf(bf16_lo(w.y), x[2], acc);
+  acc = fmaf(bf16_hi(w.y), x[3], acc);
+  acc = fmaf(bf16_lo(w.z), x[4], acc);
+  acc = fmaf(bf16_hi(w.z), x[5], acc);
+  acc = fmaf(bf16_lo(w.w), x[6], acc);
+  acc = fmaf(bf16_hi(w.w), x[7], acc);
+  return acc;
+}
+MQ_DEV float dot8_lds(uint4 w, const float* x_lds, float acc) {
+  float4 a = *reinterpret_cast<const float4*>(x_lds);
+  float4 b = *reinterpret_cast<const float4*>(x_lds + 4);
+  float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  return dot8(w, xs, acc);
+}
+MQ_DEV void unpack8(uint4 w, float* o) {
+  o[0] = bf16_lo(w.x); o[1] = bf16_hi(w.x);
+  o[2] = bf16_lo(w.y); o[3] = bf16_hi(w.y);
+  o[4] = bf16_lo(w.z); o[5] = bf16_hi(w.z);
+  o[6] = bf16_lo(w.w); o[7] = bf16_hi(w.w);
+}
+
+// ---------------------------------------------------------------------------- wave64 reductions
+// DPP control words (GCN/CDNA encoding).
+#define MQ_DPP_QUAD_XOR1 0xB1   // quad_perm [1,0,3,2]
+#define MQ_DPP_QUAD_XOR2 0x4E   // quad_perm [2,3,0,1]
+#define MQ_DPP_ROW_HALF_MIRROR 0x141
+#define MQ_DPP_ROW_MIRROR 0x140
+
+template <int CTRL>
+MQ_DEV float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over each 16-lane row; every lane of the row receives the row total.
+MQ_DEV float row16_sum(float v) {
+  v += dpp_f<MQ_DPP_QUAD_XOR1>(v);
+  v += dpp_f<MQ_DPP_QUAD_XOR2>(v);
+  v += dpp_f<MQ_DPP_ROW_HALF_MIRROR>(v);
+  v += dpp_f<MQ_DPP_ROW_MIRROR>(v);
+  return v;
+}
+MQ_DEV float row16_max(float v) {
+  v = fmaxf(v, dpp_f<MQ_DPP_QUAD_XOR1>(v));
+  v = fmaxf(v, dpp_f<MQ_DPP_QUAD_XOR2>(v));
+  v = fmaxf(v, dpp_f<MQ_DPP_ROW_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_f<MQ_DPP_ROW_MIRROR>(v));
+  return v;
+}
+// Cross-row steps go through ds_bpermute (LDS crossbar, no LDS storage).
+MQ_DEV float xor_lane(float v, int mask) {
+  int lane = __lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
+}
+// Sum over all 64 lanes; every lane receives the total.
+MQ_DEV float wave_sum(float v) {
+  v = row16_sum(v);
+  v += xor_lane(v, 16);
+  v += xor_lane(v, 32);
+  return v;
+}
+MQ_DEV float wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, xor_lane(v, 16));
+  v = fmaxf(v, xor_lane(v, 32));
+  return v;
+}
+
+// Workgroup sum of one value per thread; `red` is MQ_WAVES floats of LDS.  All threads
+// receive the total.  Contains two __syncthreads.
+MQ_DEV float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < MQ_WAVES; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+// ---------------------------------------------------------------------------- argmax keys
+// (value, index) packed so that unsigned 64-bit max picks the largest value and, among equal
+// values, the LOWEST index.  Monotone float->uint map: flip all bits of negatives, set the sign
+// bit of non-negatives.
+MQ_DEV uint64_t argmax_key(float v, uint32_t idx) {
+  uint32_t u = __float_as_uint(v);
+  uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - idx);
+}
+MQ_DEV uint32_t argmax_key_index(uint64_t k) { return 0xffffffffu - (uint32_t)(k & 0xffffffffu); }
+
+MQ_DEV uint64_t u64_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+MQ_DEV uint64_t wave_max_u64(uint64_t k) {
+  int lane = __lane_id();
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+    uint32_t olo = __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, lo);
+    uint32_t ohi = __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, hi);
+    k = u64_max(k, ((uint64_t)ohi << 32) | olo);
+  }
+  return k;
+}
+
+// ---------------------------------------------------------------------------- coherent exchange
+// Activations crossing workgroups are written and read with agent-scope relaxed atomics, which
+// gfx950 lowers to single `sc1` loads/stores that are coherent across the 8 XCD-private L2s.
+// No release/acquire fences are used: those lower to whole-L2 writeback/invalidate
+// (buffer_wbl2 / buffer_inv) and cost ~7 us per grid barrier on MI355X.  Ordering instead comes
+// from waiting for every outstanding memory operation of the wave (s_waitcnt 0) before arriving
+// at a barrier, and from issuing the data loads only after the barrier has been observed.
+MQ_DEV void st_coh(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+MQ_DEV float ld_coh(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT));
+}
+MQ_DEV float2 ld_coh2(const float* p) {
+  const uint64_t u = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
+}
+MQ_DEV void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+// ---------------------------------------------------------------------------- grid barrier
+// Sync state lives in its own 128-byte lines (one L2 line each on gfx950).
+struct alignas(128) MqLine {
+  uint32_t v;
+  uint32_t pad[31];
+};
+struct alignas(128) MqLine64 {
+  unsigned long long v;
+  uint32_t pad[30];
+};
+#define MQ_BAR_STRIPES 16
+struct MqSync {
+  MqLine bar[MQ_BAR_STRIPES];  // striped grid-barrier arrival counters (reset at step end)
+  MqLine attn[MQ_NKV];         // per-kv-head split-K completion counters (reset at step end)
+  MqLine done;                 // LM-head completion counter
+  MqLine err;                  // nonzero after a barrier timed out or a bound was violated
+  MqLine64 argmax;             // packed (value, index) key of the running vocabulary argmax
+};
+
+// Spin bound: every wave leaves a barrier after at most this many polls even if some
+// workgroup never arrives (then `err` is set and later barriers do not wait at all).
+#define MQ_SPIN_LIMIT (1u << 23)
+
+MQ_DEV uint32_t row16_sum_u32(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, MQ_DPP_QUAD_XOR1, 0xF, 0xF, true);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, MQ_DPP_QUAD_XOR2, 0xF, 0xF, true);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, MQ_DPP_ROW_HALF_MIRROR, 0xF, 0xF, true);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, MQ_DPP_ROW_MIRROR, 0xF, 0xF, true);
+  return v;
+}
+
+// Grid-wide barrier for a co-resident (cooperative) launch, executed by the sync wave only
+// (the caller brackets it with __syncthreads).  `target` is the arrival count that completes
+// this barrier: k * gridDim.x for the k-th barrier of the launch.  Workgroup w arrives on stripe
+// w % 16 (16 counters in separate lines cut the serialisation of 256 atomics on one address);
+// lanes 0..15 poll all stripes at once and sum them with DPP.  The sync wave never has weight
+// prefetches outstanding, so its polls are not queued behind them (gfx9 returns a wave's loads
+// in order).  Precondition: the compute waves have waited for the stores other workgroups will
+// read before the __syncthreads that precedes this call.
+MQ_DEV void grid_barrier_wave(MqSync* s, uint32_t target) {
+  const int lane = __lane_id();
+  if (lane == 0)
+    __hip_atomic_fetch_add(&s->bar[blockIdx.x % MQ_BAR_STRIPES].v, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t spins = 0;
+  while (true) {
+    uint32_t v = 0;
+    if (lane < MQ_BAR_STRIPES)
+      v = __hip_atomic_load(&s->bar[lane].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else if (lane == 63)
+      v = __hip_atomic_load(&s->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t e = __builtin_amdgcn_readlane(v, 63);
+    const uint32_t total = __builtin_amdgcn_readfirstlane(row16_sum_u32(v));
+    if (e != 0 || (int32_t)(total - target) >= 0) break;
+    if (++spins > MQ_SPIN_LIMIT) {
+      if (lane == 0)
+        __hip_atomic_store(&s->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+  }
+}

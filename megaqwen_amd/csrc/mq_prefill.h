@@ -1,0 +1,18 @@
+// Prefill path: buffers carved from the decoder workspace and the host launcher (prefill.hip).
+#pragma once
+
+#include "mq_decode.h"
+
+struct MqPrefillBuffers {
+  int max_n;
+  bf16_t* h;     // [n, H]    residual stream (bf16, as the reference's hidden_bf16)
+  bf16_t* xn;    // [n, H]    RMSNorm output
+  bf16_t* qkv;   // [n, 4096] q | k | v projections (q/k rotated in place)
+  bf16_t* att;   // [n, 2048] attention output
+  bf16_t* m;     // [n, 3072] silu(gate) * up
+};
+
+size_t mq_prefill_workspace_bytes(int max_n);
+void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n);
+int mq_launch_prefill(const MqDecodeParams& p, const MqPrefillBuffers& b, const int32_t* tokens,
+                      int n, int32_t* tok_out, float* logits, int grid, hipStream_t stream);

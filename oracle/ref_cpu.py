@@ -120,33 +120,43 @@ class OracleModel:
         self.position = 0
 
     # ------------------------------------------------------------------ decode
+    def decode_layer(self, li: int, x: torch.Tensor, pos: int) -> torch.Tensor:
+        """One decoder layer at position `pos` on the fp32 hidden state x [H] (bf16-valued):
+        writes K/V row `pos` of layer li and returns the layer output (rounded to bf16)."""
+        w = self.layers[li]
+        c, s = self.cos[pos], self.sin[pos]
+        cache_len = pos + 1
+        r = x
+        n = rms_norm(r, w["input_ln"])
+        q = w["q"] @ n
+        k = w["k"] @ n
+        v = w["v"] @ n
+        q = rope(rms_norm(q.view(self.nq, self.D), w["q_norm"]), c, s)      # kept fp32
+        k = rope(rms_norm(k.view(self.nkv, self.D), w["k_norm"]), c, s)
+        self.k_cache[li, :, pos] = self._r(k)
+        self.v_cache[li, :, pos] = self._r(v.view(self.nkv, self.D))
+        K = self.k_cache[li, :, :cache_len].repeat_interleave(self.group, dim=0)
+        Vv = self.v_cache[li, :, :cache_len].repeat_interleave(self.group, dim=0)
+        att = attend(q.unsqueeze(1), K, Vv, self.scale).reshape(-1)
+        a = w["o"] @ att + r
+        n2 = rms_norm(a, w["post_ln"])
+        m = silu(w["gate"] @ n2) * (w["up"] @ n2)
+        return self._r(w["down"] @ m + a)
+
+    def lm_head_logits(self, x: torch.Tensor) -> torch.Tensor:
+        """Final RMSNorm (fp32) + tied LM head (fused_decode_ldg_kernel.inl:103-137,
+        fused_decode_ldg_lm.inl:47-122)."""
+        return self.lm_head @ rms_norm(x, self.final_norm)
+
     def decode_step(self, token: int, return_logits: bool = True):
         """One decode step at the current position; returns (next_token, logits fp32 [V])."""
         pos = self.position
         if pos >= self.max_seq_len:
             raise RuntimeError("decode position exceeds max_seq_len")
-        cache_len = pos + 1
         x = self.embed[int(token)].clone()                  # bf16 row widened (kernel.inl:47-52)
-        c, s = self.cos[pos], self.sin[pos]
-        for li, w in enumerate(self.layers):
-            r = x
-            n = rms_norm(r, w["input_ln"])
-            q = w["q"] @ n
-            k = w["k"] @ n
-            v = w["v"] @ n
-            q = rope(rms_norm(q.view(self.nq, self.D), w["q_norm"]), c, s)      # kept fp32
-            k = rope(rms_norm(k.view(self.nkv, self.D), w["k_norm"]), c, s)
-            self.k_cache[li, :, pos] = self._r(k)
-            self.v_cache[li, :, pos] = self._r(v.view(self.nkv, self.D))
-            K = self.k_cache[li, :, :cache_len].repeat_interleave(self.group, dim=0)
-            Vv = self.v_cache[li, :, :cache_len].repeat_interleave(self.group, dim=0)
-            att = attend(q.unsqueeze(1), K, Vv, self.scale).reshape(-1)
-            a = w["o"] @ att + r
-            n2 = rms_norm(a, w["post_ln"])
-            m = silu(w["gate"] @ n2) * (w["up"] @ n2)
-            x = self._r(w["down"] @ m + a)
-        nf = rms_norm(x, self.final_norm)
-        logits = self.lm_head @ nf
+        for li in range(self.L):
+            x = self.decode_layer(li, x, pos)
+        logits = self.lm_head_logits(x)
         self.position += 1
         tok = int(torch.argmax(logits).item())
         return (tok, logits) if return_logits else tok

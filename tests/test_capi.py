@@ -1,0 +1,87 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function the public header
+declares, sizes buffers, and rejects bad arguments with error codes and messages."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from megaqwen_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "megaqwen_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mq_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libmegaqwen_hip.so is not built: run `python -m megaqwen_amd.build`")
+    return _lib.load()
+
+
+def test_exports_match_header(lib):
+    declared = header_functions()
+    assert declared, "no functions parsed from the header"
+    assert sorted(_lib.EXPORTED) == declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.mq_abi_version() == _lib.ABI_VERSION
+
+
+def _desc(num_layers=28, vocab=151936, max_seq=4096, max_prefill=512, hidden=1024):
+    fake = 1 << 20                                   # 16-byte aligned non-null placeholder
+    layers = (_lib.LayerWeights * num_layers)()
+    for l in range(num_layers):
+        layers[l] = _lib.LayerWeights(*[fake] * 11)
+    d = _lib.ModelDesc(hidden_size=hidden, intermediate_size=3072, num_q_heads=16, num_kv_heads=8,
+                       head_dim=128, num_layers=num_layers, vocab_size=vocab,
+                       max_seq_len=max_seq, max_prefill_len=max_prefill, embed=fake,
+                       final_norm=fake, lm_head=fake, cos_table=fake, sin_table=fake,
+                       layers=layers)
+    d._keep = layers
+    return d
+
+
+def test_sizes(lib):
+    d = _desc()
+    assert lib.mq_kv_cache_bytes(ctypes.byref(d)) == 28 * 8 * 4096 * 128 * 2
+    ws = lib.mq_workspace_bytes(ctypes.byref(d))
+    d0 = _desc(max_prefill=0)
+    ws0 = lib.mq_workspace_bytes(ctypes.byref(d0))
+    assert 0 < ws0 < ws and ws % 256 == 0
+    # prefill buffers: h, xn [n,1024], qkv [n,4096], att [n,2048], m [n,3072] in bf16
+    assert ws - ws0 >= 512 * (1024 * 2 + 4096 + 2048 + 3072) * 2
+
+
+def test_rejects_bad_shapes_and_args(lib):
+    bad = _desc(hidden=2048)
+    assert lib.mq_workspace_bytes(ctypes.byref(bad)) == 0
+    assert b"compiled Qwen3-0.6B shape" in lib.mq_last_error()
+    d = _desc(max_prefill=5000, max_seq=4096)
+    assert lib.mq_workspace_bytes(ctypes.byref(d)) == 0
+    d = _desc()
+    d.embed = 3                                      # misaligned
+    assert lib.mq_workspace_bytes(ctypes.byref(d)) == 0
+    out = ctypes.c_void_p()
+    assert lib.mq_decoder_create(ctypes.byref(_desc()), None, None, None, 0,
+                                 ctypes.byref(out)) == _lib.MQ_ERR_INVALID_ARG
+    assert out.value is None
+    assert lib.mq_decode_step(None, None, None, None, None) == _lib.MQ_ERR_INVALID_ARG
+    assert lib.mq_prefill(None, None, 0, None, None, None) == _lib.MQ_ERR_INVALID_ARG
+    assert lib.mq_decoder_position(None) == -1
+    with pytest.raises(_lib.MegaQwenError):
+        _lib.check(lib.mq_decoder_reset(None, None))
+
+
+def test_decoder_requires_cuda_tensors():
+    import torch
+    from megaqwen_amd.decoder import MegakernelDecoder
+    t = torch.zeros(4, dtype=torch.bfloat16)
+    with pytest.raises((TypeError, ValueError)):
+        MegakernelDecoder(t, [t] * 11, t, t, t, t, 1, 16)

@@ -1,0 +1,232 @@
+"""Full-model decode parity: HIP decoder (persistent and multi-kernel) against the CPU oracle.
+
+The oracle (oracle/ref_cpu.py, decode mode with the reference's bf16 rounding points) runs on the
+same seeded bf16 weights and bf16 RoPE tables.  Teacher-forced: both consume the same input
+tokens, so every step's logits are compared (max-abs <= 2e-2) and the GPU greedy
+token must equal the oracle's wherever the oracle's top-2 margin exceeds twice the observed
+logit error.
+"""
+import pytest
+import torch
+
+from megaqwen_amd.synthetic import make_tokens
+from tests.helpers import build_pair, top2_margin
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _run_teacher_forced(dec, orc, tokens, mode):
+    dec.set_mode(mode)
+    dec.reset()
+    orc.reset()
+    worst = 0.0
+    for i, t in enumerate(tokens):
+        tok, lg = dec.decode_step_with_logits(int(t))
+        otok, olg = orc.decode_step(int(t))
+        err = float((lg.cpu() - olg).abs().max())
+        worst = max(worst, err)
+        assert err <= TOL, (mode, i, err)
+        if top2_margin(olg) > 2 * err + 1e-6:
+            assert tok == otok, (mode, i, tok, otok)
+        assert dec.position() == i + 1
+    dec.check()
+    return worst
+
+
+@pytest.fixture(scope="module")
+def small():
+    return build_pair(2, 151936, 512, seed=1, norm_jitter=0.1)
+
+
+@pytest.mark.parametrize("mode", ["persistent", "multi_kernel"])
+def test_decode_2layer_teacher_forced(small, mode):
+    dec, orc, sp, _ = small
+    toks = make_tokens(80, sp["vocab_size"], seed=3)
+    _run_teacher_forced(dec, orc, toks, mode)
+
+
+def test_decode_modes_bitwise_identical_and_deterministic(small):
+    dec, _, sp, _ = small
+    toks = make_tokens(20, sp["vocab_size"], seed=4)
+    outs = []
+    for mode in ("persistent", "persistent", "multi_kernel"):
+        dec.set_mode(mode)
+        dec.reset()
+        outs.append(torch.stack([dec.decode_step_with_logits(int(t))[1] for t in toks]))
+    assert torch.equal(outs[0], outs[1])     # run-to-run determinism (doubles as race check)
+    assert torch.equal(outs[0], outs[2])     # same arithmetic in both kernel organisations
+
+
+def test_decode_long_context_chunks(small):
+    """Positions up to 511: several split-K chunks per kv head, merge exercised every layer."""
+    dec, orc, sp, _ = small
+    toks = make_tokens(512, sp["vocab_size"], seed=5)
+    dec.set_mode("persistent")
+    dec.reset()
+    orc.reset()
+    for i, t in enumerate(toks):
+        if i % 50 == 0 or i >= 505:
+            tok, lg = dec.decode_step_with_logits(int(t))
+            otok, olg = orc.decode_step(int(t))
+            assert float((lg.cpu() - olg).abs().max()) <= TOL, i
+        else:
+            dec.decode_step(int(t))
+            orc.decode_step(int(t), return_logits=False)
+    with pytest.raises(RuntimeError):
+        dec.decode_step(1)                       # position == max_seq_len: host bound check
+    dec.check()
+
+
+def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    e = torch.floor(torch.log2(x.abs().clamp_min(1e-30)))
+    return torch.pow(2.0, e - 7)
+
+
+@pytest.fixture(scope="module")
+def full():
+    return build_pair(28, 151936, 64, seed=0)
+
+
+def _layer_fp64(orc, li, x, pos, kc, vc):
+    """Layer li of the oracle recomputed in float64 from the same inputs (diagnostics)."""
+    from oracle.ref_cpu import attend, rms_norm, rope, silu
+    w = {k: v.double() for k, v in orc.layers[li].items()}
+    c, s = orc.cos[pos].double(), orc.sin[pos].double()
+    x = x.double()
+    n = rms_norm(x, w["input_ln"])
+    q = rope(rms_norm((w["q"] @ n).view(16, 128), w["q_norm"]), c, s)
+    k = rope(rms_norm((w["k"] @ n).view(8, 128), w["k_norm"]), c, s)
+    v = (w["v"] @ n).view(8, 128)
+    K = kc[li, :, :pos + 1].double().clone()
+    V = vc[li, :, :pos + 1].double().clone()
+    K[:, pos] = k.float().to(torch.bfloat16).double()
+    V[:, pos] = v.float().to(torch.bfloat16).double()
+    att = attend(q.unsqueeze(1), K.repeat_interleave(2, 0), V.repeat_interleave(2, 0),
+                 orc.scale).reshape(-1)
+    a = w["o"] @ att + x
+    n2 = rms_norm(a, w["post_ln"])
+    return w["down"] @ (silu(w["gate"] @ n2) * (w["up"] @ n2)) + a
+
+
+def test_decode_28_layers_layerwise(full):
+    """The real configuration (28 layers, vocab 151936, N(0, 0.02) weights, unit norms), checked
+    layer by layer: each oracle layer consumes the GPU's hidden state from the layer before and
+    the GPU's KV cache, so rounding-order differences cannot compound across layers.  Every
+    layer output must be within one bf16 ulp of the oracle (nearly all bit-equal), and the
+    logits computed from the GPU's last hidden state within 1e-4.  The per-element bound is one
+    bf16 ulp plus an fp32-accumulation floor of 2e-5 x max|layer output| (a layer output is a
+    sum of O(1) terms; where they cancel, fp32 reordering alone can move the sum across a bf16
+    rounding boundary by more than one ulp of the small result)."""
+    dec, orc, sp, _ = full
+    dec.set_mode("persistent")
+    dec.reset()
+    toks = make_tokens(6, sp["vocab_size"], seed=0).tolist()
+    for step, t in enumerate(toks):
+        kcache = dec.k_cache.float().cpu()
+        vcache = dec.v_cache.float().cpu()
+        orc.k_cache.copy_(kcache)
+        orc.v_cache.copy_(vcache)
+        tok, lg, trace = dec.debug_decode_step_layers(t)
+        trace = trace.cpu()
+        x = orc.embed[t].clone()
+        exact = 0
+        for li in range(sp["num_layers"]):
+            y = orc.decode_layer(li, x, step)
+            g = trace[li]
+            bound = _bf16_ulp(y) + 2e-5 * float(y.abs().max())
+            bad = (g - y).abs() > bound
+            if bad.any():
+                z = _layer_fp64(orc, li, x, step, kcache, vcache)
+                print(f"step {step} layer {li}: gpu {g[bad][:4].tolist()} oracle32 "
+                      f"{y[bad][:4].tolist()} fp64-unrounded {z[bad][:4].tolist()}")
+            assert not bad.any(), (step, li, g[bad][:4].tolist(), y[bad][:4].tolist())
+            exact += int((g == y).sum())
+            x = g                       # teacher-force the GPU's hidden state
+        assert exact >= 0.99 * sp["num_layers"] * 1024, (step, exact)
+        ref = orc.lm_head_logits(trace[-1])
+        assert float((lg.cpu() - ref).abs().max()) < 1e-4, step
+        assert tok == int(torch.argmax(lg))
+        kc = dec.k_cache[:, :, step].float().cpu()
+        assert ((kc - orc.k_cache[:, :, step]).abs() <= _bf16_ulp(orc.k_cache[:, :, step]) + 1e-30).all()
+    dec.check()
+
+
+def test_decode_28_layers_free_running(full):
+    """Free-running teacher-forced comparison of the full 28-layer model.  At this depth the
+    random-init model amplifies a single bf16-ulp flip of one hidden element to ~3e-2 on the
+    logits, and the oracle's own fp32 and fp64 evaluations differ by ~2.7e-2, so the bound here
+    is 6e-2 (about twice that intrinsic spread); the 2e-2 bar is enforced by the 2-layer tests
+    above and the layer-by-layer test."""
+    dec, orc, sp, _ = full
+    toks = make_tokens(8, sp["vocab_size"], seed=0)
+    dec.set_mode("persistent")
+    dec.reset()
+    orc.reset()
+    worst = 0.0
+    for i, t in enumerate(toks):
+        tok, lg = dec.decode_step_with_logits(int(t))
+        otok, olg = orc.decode_step(int(t))
+        err = float((lg.cpu() - olg).abs().max())
+        worst = max(worst, err)
+        assert err <= 6e-2, (i, err)
+        if top2_margin(olg) > 2 * err + 1e-6:
+            assert tok == otok, (i, tok, otok)
+    print(f"28-layer free-running worst logit error {worst:.3e}")
+    dec.check()
+
+
+def test_decode_steps_chain_and_graph(small):
+    dec, _, sp, _ = small
+    first = int(make_tokens(1, sp["vocab_size"], seed=6)[0])
+    dec.set_mode("persistent")
+    dec.reset()
+    ref = []
+    t = first
+    for _ in range(24):
+        t = dec.decode_step(t)
+        ref.append(t)
+    dec.reset()
+    chain = dec.decode_steps_cuda(first, 24).cpu().tolist()
+    assert chain == ref and dec.position() == 24
+    dec.reset()
+    host = dec.decode_steps(first, 24).tolist()
+    assert host == ref
+    dec.reset()
+    g1 = dec.decode_steps_cuda_graph(first, 12).cpu().tolist()
+    torch.cuda.synchronize()
+    g2 = dec.decode_steps_cuda_graph(g1[-1], 12).cpu().tolist()
+    assert g1 + g2 == ref and dec.position() == 24
+    dec.check()
+
+
+def test_decode_greedy_cuda_eos(small):
+    dec, _, sp, _ = small
+    first = int(make_tokens(1, sp["vocab_size"], seed=7)[0])
+    dec.reset()
+    seq = [first] + dec.decode_steps_cuda(first, 40).cpu().tolist()
+    eos = seq[17]
+    stop_at = seq.index(eos, 1)
+    dec.reset()
+    out, k, code = dec.decode_greedy_cuda(first, 40, [eos], chunk=8)
+    assert code == 1 and k == stop_at and out.cpu().tolist() == seq[:stop_at]
+    dec.reset()
+    out, k, code = dec.decode_greedy_cuda(first, 30, [-5], chunk=7)
+    assert code == 0 and k == 30 and out.cpu().tolist() == seq[:30]
+
+
+def test_reset_and_position_semantics(small):
+    dec, _, sp, _ = small
+    dec.reset()
+    assert dec.position() == 0
+    a = dec.decode_step(5)
+    dec.decode_step(a)
+    assert dec.position() == 2
+    assert float(dec.get_k_cache()[:, :, :2].float().abs().sum()) > 0
+    dec.reset()
+    assert dec.position() == 0
+    assert float(dec.get_k_cache().float().abs().sum()) == 0.0
+    assert dec.decode_step(5) == a
+    with pytest.raises(ValueError):
+        dec.decode_step(sp["vocab_size"])
