@@ -155,19 +155,30 @@ MQ_DEV void wave_copy_bf16_1024(float* dst, const bf16_t* src) {
   for (int i = 0; i < 2; ++i) unpack8(v[i], dst + 8 * (lane + 64 * i));
 }
 
-// Phase boundary.  Compute waves arrive after publishing (and waiting for) their outputs and
-// issuing the next phase's prefetch.  The sync wave runs the grid barrier (when `barrier`) and
-// then `input()` (loads of the next phase's input into LDS).
-template <class Input>
-MQ_DEV void phase_sync(MqSync* sy, uint32_t target, bool barrier, Input input) {
+// Phase boundary.  Compute waves arrive with this phase's dot products in LDS and the next
+// phase's weight prefetch in flight.  The sync wave then runs `epilogue()` (finishes this
+// phase's outputs and publishes them with coherent stores), waits for those stores, runs the
+// grid barrier (when `barrier`) and `input()` (the next phase's input vector into LDS).  The
+// compute waves never wait for a store, so their prefetches are never waited on either.
+template <class Epi, class Input>
+MQ_DEV void phase_sync(MqSync* sy, uint32_t target, bool barrier, Epi epilogue, Input input) {
   __syncthreads();
   if (wave_id() == MQ_SYNC_WAVE) {
+    epilogue();
+    wait_all_memory();
     if (barrier) grid_barrier_wave(sy, target);
     input();
     wait_all_memory();
   }
   __syncthreads();
 }
+// End of a single-phase kernel: the sync wave publishes the phase's outputs.
+template <class Epi>
+MQ_DEV void phase_finish(Epi epilogue) {
+  __syncthreads();
+  if (wave_id() == MQ_SYNC_WAVE) epilogue();
+}
+#define MQ_NOTHING [] {}
 
 // ---------------------------------------------------------------------------- RMSNorm
 // xn = x * rsqrt(mean(x^2) + eps) * w over the 1024 values in LDS `x`, two per thread.
@@ -189,14 +200,20 @@ MQ_DEV void qkv_load(QkvSet& ws, const MqLayerW& w, int wg, int G) {
   row_range(MQ_QKV, wg, G, r0, nr);
   ws.load([&](int i) { return qkv_row(w, r0 + i); }, nr);
 }
-// Input: the layer input x in LDS_IN.
-MQ_DEV void qkv_run(const QkvSet& ws, const MqLayerW& w, float* qkv, int wg, int G, float* lds) {
+// Input: the layer input x in LDS_IN; dot products -> LDS_PR.
+MQ_DEV void qkv_run(const QkvSet& ws, const MqLayerW& w, int wg, int G, float* lds) {
   norm_1024(lds + LDS_IN, w.in_ln, lds + LDS_XN, lds + LDS_RED);
   __syncthreads();
   int r0, nr;
   row_range(MQ_QKV, wg, G, r0, nr);
   ws.compute([&](int i) { return qkv_row(w, r0 + i); }, nr, lds + LDS_XN,
-             [&](int it, float v) { st_coh(qkv + r0 + it, v); });
+             [&](int it, float v) { lds[LDS_PR + it] = v; });
+}
+// Sync-wave epilogue: publish q|k|v rows.
+MQ_DEV void qkv_publish(float* qkv, int wg, int G, const float* lds) {
+  int r0, nr;
+  row_range(MQ_QKV, wg, G, r0, nr);
+  for (int t = lane_id(); t < nr; t += 64) st_coh(qkv + r0 + t, lds[LDS_PR + t]);
 }
 
 // ------------------------------------------------------------------------- P2: attention
@@ -567,19 +584,22 @@ MQ_DEV void o_load(OSet& ws, const MqLayerW& w, int wg, int G) {
   row_range(MQ_H, wg, G, r0, nr);
   ws.load([&](int i) { return w.wo + (size_t)(r0 + i) * MQ_QDIM; }, nr);
 }
-// Input: att in LDS_IN.  Thread t < nr holds the residual of hidden row r0 + t in `res` and
-// receives a[r0 + t] in it.
-MQ_DEV void o_run(const OSet& ws, const MqLayerW& w, float* a_out, int wg, int G, float* lds,
-                  float& res) {
-  float* pr = lds + LDS_PR;
+// Input: att in LDS_IN; segment dot products -> LDS_PR.
+MQ_DEV void o_run(const OSet& ws, const MqLayerW& w, int wg, int G, float* lds) {
   int r0, nr;
   row_range(MQ_H, wg, G, r0, nr);
   ws.compute([&](int i) { return w.wo + (size_t)(r0 + i) * MQ_QDIM; }, nr, lds + LDS_IN,
-             [&](int it, float v) { pr[it] = v; });
-  __syncthreads();
-  if (tid() < nr) {
-    res = (pr[2 * tid()] + pr[2 * tid() + 1]) + res;
-    st_coh(a_out + r0 + tid(), res);
+             [&](int it, float v) { lds[LDS_PR + it] = v; });
+}
+// Sync-wave epilogue: lane t < nr (<= 64) holds the residual of hidden row r0 + t in `res`
+// and leaves a[r0 + t] = W_o att + res in it (fused_decode_ldg_mlp.inl:24-68).
+MQ_DEV void o_publish(float* a_out, int wg, int G, const float* lds, float& res) {
+  int r0, nr;
+  row_range(MQ_H, wg, G, r0, nr);
+  const int t = lane_id();
+  if (t < nr) {
+    res = (lds[LDS_PR + 2 * t] + lds[LDS_PR + 2 * t + 1]) + res;
+    st_coh(a_out + r0 + t, res);
   }
 }
 
@@ -591,20 +611,24 @@ MQ_DEV void gu_load(GateUpSet& ws, const MqLayerW& w, int wg, int G) {
     return i < nr ? w.wg + (size_t)(r0 + i) * MQ_H : w.wu + (size_t)(r0 + i - nr) * MQ_H;
   }, 2 * nr);
 }
-// Input: a in LDS_IN.
-MQ_DEV void gu_run(const GateUpSet& ws, const MqLayerW& w, float* m, int wg, int G, float* lds) {
-  float* pr = lds + LDS_PR;
+// Input: a in LDS_IN; gate and up dot products -> LDS_PR.
+MQ_DEV void gu_run(const GateUpSet& ws, const MqLayerW& w, int wg, int G, float* lds) {
   norm_1024(lds + LDS_IN, w.post_ln, lds + LDS_XN, lds + LDS_RED);
   __syncthreads();
   int r0, nr;
   row_range(MQ_I, wg, G, r0, nr);
   ws.compute([&](int i) {
     return i < nr ? w.wg + (size_t)(r0 + i) * MQ_H : w.wu + (size_t)(r0 + i - nr) * MQ_H;
-  }, 2 * nr, lds + LDS_XN, [&](int it, float v) { pr[it] = v; });
-  __syncthreads();
-  if (tid() < nr) {
-    const float gv = pr[tid()], uv = pr[nr + tid()];
-    st_coh(m + r0 + tid(), gv / (1.0f + expf(-gv)) * uv);
+  }, 2 * nr, lds + LDS_XN, [&](int it, float v) { lds[LDS_PR + it] = v; });
+}
+// Sync-wave epilogue: m = silu(g) * u with silu(x) = x / (1 + e^-x)
+// (fused_decode_ldg_mlp.inl:120-175, fused_decode_ldg_common.inl:123-125).
+MQ_DEV void gu_publish(float* m, int wg, int G, const float* lds) {
+  int r0, nr;
+  row_range(MQ_I, wg, G, r0, nr);
+  for (int t = lane_id(); t < nr; t += 64) {
+    const float gv = lds[LDS_PR + t], uv = lds[LDS_PR + nr + t];
+    st_coh(m + r0 + t, gv / (1.0f + expf(-gv)) * uv);
   }
 }
 
@@ -614,20 +638,23 @@ MQ_DEV void down_load(DownSet& ws, const MqLayerW& w, int wg, int G) {
   row_range(MQ_H, wg, G, r0, nr);
   ws.load([&](int i) { return w.wd + (size_t)(r0 + i) * MQ_I; }, nr);
 }
-// Input: m in LDS_IN.  Thread t < nr holds a[r0 + t] in `res` and receives the bf16-rounded
-// layer output of that row in it; out(r, v) publishes it.
-template <class Out>
-MQ_DEV void down_run(const DownSet& ws, const MqLayerW& w, int wg, int G, float* lds, float& res,
-                     Out out) {
-  float* pr = lds + LDS_PR;
+// Input: m in LDS_IN; segment dot products -> LDS_PR.
+MQ_DEV void down_run(const DownSet& ws, const MqLayerW& w, int wg, int G, float* lds) {
   int r0, nr;
   row_range(MQ_H, wg, G, r0, nr);
   ws.compute([&](int i) { return w.wd + (size_t)(r0 + i) * MQ_I; }, nr, lds + LDS_IN,
-             [&](int it, float v) { pr[it] = v; });
-  __syncthreads();
-  if (tid() < nr) {
-    res = round_bf16((pr[2 * tid()] + pr[2 * tid() + 1]) + res);
-    out(r0 + tid(), res);
+             [&](int it, float v) { lds[LDS_PR + it] = v; });
+}
+// Sync-wave epilogue: lane t < nr holds a[r0 + t] in `res` and leaves the bf16-rounded layer
+// output of that row in it (fused_decode_ldg_mlp.inl:177-217); out(r, v) publishes it.
+template <class Out>
+MQ_DEV void down_publish(int wg, int G, const float* lds, float& res, Out out) {
+  int r0, nr;
+  row_range(MQ_H, wg, G, r0, nr);
+  const int t = lane_id();
+  if (t < nr) {
+    res = round_bf16((lds[LDS_PR + 2 * t] + lds[LDS_PR + 2 * t + 1]) + res);
+    out(r0 + t, res);
   }
 }
 
@@ -743,7 +770,8 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
   const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
   int r0h, nrh;
   row_range(MQ_H, wg, G, r0h, nrh);
-  float res = tid() < nrh ? bf16_to_f32(xe[r0h + tid()]) : 0.f;   // residual of my hidden rows
+  // residual of this workgroup's hidden rows, held by sync-wave lane t for row r0h + t
+  float res = lane_id() < nrh ? bf16_to_f32(xe[r0h + lane_id()]) : 0.f;
   uint32_t nbar = 0;
   QkvSet wq;
   OSet wo;
@@ -751,46 +779,44 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
   DownSet wd;
   KvBlock kv;
   qkv_load(wq, p.layers[0], wg, G);
-  phase_sync(sy, 0, false, [&] { wave_copy_bf16_1024(lds + LDS_IN, xe); });
+  phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_bf16_1024(lds + LDS_IN, xe); });
   for (int l = 0; l < p.num_layers; ++l) {
     const MqLayerW w = p.layers[l];
     stamp(p, wg, l, 0);
-    qkv_run(wq, w, s->qkv, wg, G, lds);
-    wait_all_memory();
+    qkv_run(wq, w, wg, G, lds);
     stamp(p, wg, l, 1);
     if (item.active)
       kv_block_load(kv, kv_base(p.kc, p, l, item.h), kv_base(p.vc, p, l, item.h), item.p0,
                     min(item.p1, item.p0 + MQ_ATT_BLOCK));
-    phase_sync(sy, (++nbar) * (uint32_t)G, true, [&] {
-      if (item.active) attn_input(s->qkv, item.h, lds);
-    });
+    phase_sync(sy, (++nbar) * (uint32_t)G, true, [&] { qkv_publish(s->qkv, wg, G, lds); },
+               [&] { if (item.active) attn_input(s->qkv, item.h, lds); });
     stamp(p, wg, l, 2);
-    if (item.active) attn_run(p, l, w, pos, nch, item, kv, lds);
-    wait_all_memory();
+    if (item.active) {
+      attn_run(p, l, w, pos, nch, item, kv, lds);
+      wait_all_memory();
+    }
     stamp(p, wg, l, 3);
     o_load(wo, w, wg, G);
-    phase_sync(sy, (++nbar) * (uint32_t)G, true,
+    phase_sync(sy, (++nbar) * (uint32_t)G, true, MQ_NOTHING,
                [&] { wave_copy_coh<MQ_QDIM>(lds + LDS_IN, s->att); });
     stamp(p, wg, l, 4);
-    o_run(wo, w, s->a, wg, G, lds, res);
-    wait_all_memory();
+    o_run(wo, w, wg, G, lds);
     stamp(p, wg, l, 5);
     gu_load(wgu, w, wg, G);
-    phase_sync(sy, (++nbar) * (uint32_t)G, true,
+    phase_sync(sy, (++nbar) * (uint32_t)G, true, [&] { o_publish(s->a, wg, G, lds, res); },
                [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, s->a); });
     stamp(p, wg, l, 6);
-    gu_run(wgu, w, s->mlp, wg, G, lds);
-    wait_all_memory();
+    gu_run(wgu, w, wg, G, lds);
     stamp(p, wg, l, 7);
     down_load(wd, w, wg, G);
-    phase_sync(sy, (++nbar) * (uint32_t)G, true,
+    phase_sync(sy, (++nbar) * (uint32_t)G, true, [&] { gu_publish(s->mlp, wg, G, lds); },
                [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, s->mlp); });
     stamp(p, wg, l, 8);
-    down_run(wd, w, wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); });
-    wait_all_memory();
+    down_run(wd, w, wg, G, lds);
     stamp(p, wg, l, 9);
     if (l + 1 < p.num_layers) qkv_load(wq, p.layers[l + 1], wg, G);
     phase_sync(sy, (++nbar) * (uint32_t)G, true,
+               [&] { down_publish(wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); }); },
                [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, s->hidden); });
     stamp(p, wg, l, 10);
   }
@@ -809,8 +835,9 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
   const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
   int r0h, nrh;
   row_range(MQ_H, wg, G, r0h, nrh);
+  const int t = lane_id();
   if constexpr (PH == 5) {
-    phase_sync(sy, 0, false, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, s->hidden); });
+    phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, s->hidden); });
     lm_head_run(p, wg, G, lds, p.tok_out, p.logits, pos, true);
   } else {
     const MqLayerW w = p.layers[l];
@@ -818,11 +845,12 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
     if constexpr (PH == 0) {
       QkvSet ws;
       qkv_load(ws, w, wg, G);
-      phase_sync(sy, 0, false, [&] {
+      phase_sync(sy, 0, false, MQ_NOTHING, [&] {
         if (l == 0) wave_copy_bf16_1024(lds + LDS_IN, xe);
         else wave_copy_coh<MQ_H>(lds + LDS_IN, s->hidden);
       });
-      qkv_run(ws, w, s->qkv, wg, G, lds);
+      qkv_run(ws, w, wg, G, lds);
+      phase_finish([&] { qkv_publish(s->qkv, wg, G, lds); });
     }
     if constexpr (PH == 1) {
       const AttnItem item = attn_item(wg, nch, pos + 1);
@@ -830,7 +858,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
         KvBlock kv;
         kv_block_load(kv, kv_base(p.kc, p, l, item.h), kv_base(p.vc, p, l, item.h), item.p0,
                       min(item.p1, item.p0 + MQ_ATT_BLOCK));
-        phase_sync(sy, 0, false, [&] { attn_input(s->qkv, item.h, lds); });
+        phase_sync(sy, 0, false, MQ_NOTHING, [&] { attn_input(s->qkv, item.h, lds); });
         attn_run(p, l, w, pos, nch, item, kv, lds);
       }
     }
@@ -838,23 +866,28 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       OSet ws;
       o_load(ws, w, wg, G);
       float res = 0.f;
-      if (tid() < nrh)
-        res = l == 0 ? bf16_to_f32(xe[r0h + tid()]) : ld_coh(s->hidden + r0h + tid());
-      phase_sync(sy, 0, false, [&] { wave_copy_coh<MQ_QDIM>(lds + LDS_IN, s->att); });
-      o_run(ws, w, s->a, wg, G, lds, res);
+      if (t < nrh) res = l == 0 ? bf16_to_f32(xe[r0h + t]) : ld_coh(s->hidden + r0h + t);
+      phase_sync(sy, 0, false, MQ_NOTHING,
+                 [&] { wave_copy_coh<MQ_QDIM>(lds + LDS_IN, s->att); });
+      o_run(ws, w, wg, G, lds);
+      phase_finish([&] { o_publish(s->a, wg, G, lds, res); });
     }
     if constexpr (PH == 3) {
       GateUpSet ws;
       gu_load(ws, w, wg, G);
-      phase_sync(sy, 0, false, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, s->a); });
-      gu_run(ws, w, s->mlp, wg, G, lds);
+      phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, s->a); });
+      gu_run(ws, w, wg, G, lds);
+      phase_finish([&] { gu_publish(s->mlp, wg, G, lds); });
     }
     if constexpr (PH == 4) {
       DownSet ws;
       down_load(ws, w, wg, G);
-      float res = tid() < nrh ? ld_coh(s->a + r0h + tid()) : 0.f;
-      phase_sync(sy, 0, false, [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, s->mlp); });
-      down_run(ws, w, wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); });
+      float res = t < nrh ? ld_coh(s->a + r0h + t) : 0.f;
+      phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, s->mlp); });
+      down_run(ws, w, wg, G, lds);
+      phase_finish([&] {
+        down_publish(wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); });
+      });
     }
   }
 }
@@ -866,14 +899,15 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_qkv_kernel(MqDecodeParams p,
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   QkvSet ws;
   qkv_load(ws, p.layers[l], blockIdx.x, gridDim.x);
-  phase_sync(&p.st->sync, 0, false, [&] { wave_copy_bf16_1024(lds + LDS_IN, x); });
-  qkv_run(ws, p.layers[l], p.s->qkv, blockIdx.x, gridDim.x, lds);
+  phase_sync(&p.st->sync, 0, false, MQ_NOTHING, [&] { wave_copy_bf16_1024(lds + LDS_IN, x); });
+  qkv_run(ws, p.layers[l], blockIdx.x, gridDim.x, lds);
+  phase_finish([&] { qkv_publish(p.s->qkv, blockIdx.x, gridDim.x, lds); });
 }
 __global__ void __launch_bounds__(MQ_THREADS) mq_op_rope_kernel(MqDecodeParams p, int l, int pos,
                                                                  float* q_out) {
   __shared__ __align__(16) float lds[1024];
   const int h = blockIdx.x;
-  phase_sync(&p.st->sync, 0, false, [&] { attn_input(p.s->qkv, h, lds); });
+  phase_sync(&p.st->sync, 0, false, MQ_NOTHING, [&] { attn_input(p.s->qkv, h, lds); });
   attn_prologue(p, l, p.layers[l], h, pos, true, lds);
   __syncthreads();
   if (tid() < 256) q_out[2 * h * MQ_D + tid()] = lds[ALDS_QS + tid()];
@@ -905,8 +939,9 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_gateup_kernel(MqDecodeParams
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   GateUpSet ws;
   gu_load(ws, p.layers[l], blockIdx.x, gridDim.x);
-  phase_sync(&p.st->sync, 0, false, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, a); });
-  gu_run(ws, p.layers[l], p.s->mlp, blockIdx.x, gridDim.x, lds);
+  phase_sync(&p.st->sync, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, a); });
+  gu_run(ws, p.layers[l], blockIdx.x, gridDim.x, lds);
+  phase_finish([&] { gu_publish(p.s->mlp, blockIdx.x, gridDim.x, lds); });
 }
 __global__ void __launch_bounds__(MQ_THREADS) mq_op_down_kernel(MqDecodeParams p, int l,
                                                                  const float* a, bf16_t* x_out) {
@@ -915,16 +950,21 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_down_kernel(MqDecodeParams p
   down_load(ws, p.layers[l], blockIdx.x, gridDim.x);
   int r0, nr;
   row_range(MQ_H, blockIdx.x, gridDim.x, r0, nr);
-  float res = tid() < nr ? ld_coh(a + r0 + tid()) : 0.f;
-  phase_sync(&p.st->sync, 0, false, [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, p.s->mlp); });
-  down_run(ws, p.layers[l], blockIdx.x, gridDim.x, lds, res,
-           [&](int r, float v) { x_out[r] = f32_to_bf16(v); });
+  float res = lane_id() < nr ? ld_coh(a + r0 + lane_id()) : 0.f;
+  phase_sync(&p.st->sync, 0, false, MQ_NOTHING,
+             [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, p.s->mlp); });
+  down_run(ws, p.layers[l], blockIdx.x, gridDim.x, lds);
+  phase_finish([&] {
+    down_publish(blockIdx.x, gridDim.x, lds, res,
+                 [&](int r, float v) { x_out[r] = f32_to_bf16(v); });
+  });
 }
 // (d) final RMSNorm + LM head + argmax of a given bf16 hidden state.
 __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, const bf16_t* x,
                                                                int* tok_out, float* logits) {
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
-  phase_sync(&p.st->sync, 0, false, [&] { wave_copy_bf16_1024(lds + LDS_IN, x); });
+  phase_sync(&p.st->sync, 0, false, MQ_NOTHING,
+             [&] { wave_copy_bf16_1024(lds + LDS_IN, x); });
   lm_head_run(p, blockIdx.x, gridDim.x, lds, tok_out, logits, 0, false);
 }
 

@@ -120,9 +120,10 @@ class OracleModel:
         self.position = 0
 
     # ------------------------------------------------------------------ decode
-    def decode_layer(self, li: int, x: torch.Tensor, pos: int) -> torch.Tensor:
+    def decode_layer(self, li: int, x: torch.Tensor, pos: int, write_kv: bool = True) -> torch.Tensor:
         """One decoder layer at position `pos` on the fp32 hidden state x [H] (bf16-valued):
-        writes K/V row `pos` of layer li and returns the layer output (rounded to bf16)."""
+        writes K/V row `pos` of layer li (unless `write_kv` is False, in which case the row
+        already in the cache is used) and returns the layer output (rounded to bf16)."""
         w = self.layers[li]
         c, s = self.cos[pos], self.sin[pos]
         cache_len = pos + 1
@@ -133,8 +134,9 @@ class OracleModel:
         v = w["v"] @ n
         q = rope(rms_norm(q.view(self.nq, self.D), w["q_norm"]), c, s)      # kept fp32
         k = rope(rms_norm(k.view(self.nkv, self.D), w["k_norm"]), c, s)
-        self.k_cache[li, :, pos] = self._r(k)
-        self.v_cache[li, :, pos] = self._r(v.view(self.nkv, self.D))
+        if write_kv:
+            self.k_cache[li, :, pos] = self._r(k)
+            self.v_cache[li, :, pos] = self._r(v.view(self.nkv, self.D))
         K = self.k_cache[li, :, :cache_len].repeat_interleave(self.group, dim=0)
         Vv = self.v_cache[li, :, :cache_len].repeat_interleave(self.group, dim=0)
         att = attend(q.unsqueeze(1), K, Vv, self.scale).reshape(-1)
