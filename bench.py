@@ -6,8 +6,14 @@ Workload: Qwen3-0.6B architecture (28 layers, hidden 1024, 16/8 heads x 128, MLP
 151936, tied LM head), seeded N(0, 0.02) bf16 weights (megaqwen_amd.synthetic, seed 0), batch 1,
 greedy decode.  A step is one decoded token (one persistent decode kernel launch).  Exactly K
 steps are timed at each position bucket: positions 1..K, 128..127+K (the headline `value`) and
-4096..4095+K; the KV cache is filled to the bucket start with untimed decode steps.  Inputs are
-resident in HBM; the timed region is a device-side token chain (no host round trip per token).
+4096..4095+K; each bucket starts from an untimed prefill of that many uniform-random tokens
+(seed 1), as BASELINE config 5 does for 4096.  Inputs are resident in HBM; the timed region is a
+device-side token chain (no host round trip per token).
+
+Prefill: a 512-token uniform-random prompt (seed 1) through the MFMA prefill,
+reported as tokens/s and MFMA utilisation = 481.4 GFLOP (linear 450.97 + causal attention 30.12 +
+last-token LM head 0.31) / time / 2.5 PFLOP/s dense bf16; the 4096-token prefill time is
+reported too.
 
 Roofline: algorithmic bytes per token = bf16 weights streamed (1,192,101,888 B) + KV read
 (114,688 B x (pos + 1)) + KV write (114,688 B), over the per-launch duration measured with HIP
@@ -37,7 +43,18 @@ def bytes_per_token(pos: int) -> int:
     return WEIGHT_BYTES + KV_BYTES_PER_POS * (pos + 1) + KV_BYTES_PER_POS
 
 
-def build_decoder(max_seq: int):
+MFMA_BF16_PEAK = 2.5e15
+LINEAR_PARAMS_PER_LAYER = 4096 * 1024 + 1024 * 2048 + 2 * 3072 * 1024 + 1024 * 3072
+
+
+def prefill_flops(n: int) -> float:
+    linear = 2.0 * n * LINEAR_PARAMS_PER_LAYER * 28
+    attention = 28 * 16 * (n * (n + 1) / 2) * 128 * 4
+    lm_head = 2.0 * 151936 * 1024
+    return linear + attention + lm_head
+
+
+def build_decoder(max_seq: int, max_prefill: int = 0):
     import torch
     from megaqwen_amd.decoder import MegakernelPrefillDecoder
     from megaqwen_amd.rope import build_rope_tables
@@ -50,19 +67,18 @@ def build_decoder(max_seq: int):
     emb = w["embed_weight"].cuda()
     layers = [t.cuda() for t in w["layer_weights"]]
     dec = MegakernelPrefillDecoder(emb, layers, w["final_norm_weight"].cuda(), emb, cos.cuda(),
-                                   sin.cuda(), spec["num_layers"], max_seq, max_prefill_len=0)
+                                   sin.cuda(), spec["num_layers"], max_seq,
+                                   max_prefill_len=max_prefill)
     return dec, spec
 
 
-def time_bucket(dec, start_pos: int, steps: int, first_token: int):
-    """Fills the cache to `start_pos`, then times `steps` decode launches one by one with event
-    pairs (per-launch duration) inside one region bracketed by synchronize (wall time)."""
+def time_bucket(dec, start_pos: int, steps: int):
+    """Prefills `start_pos` random tokens, then times `steps` decode launches one by one with
+    event pairs (per-launch duration) inside one region bracketed by synchronize (wall time)."""
     import torch
+    from megaqwen_amd.synthetic import make_tokens
     dec.reset()
-    tok = first_token
-    if start_pos > 0:
-        toks = dec.decode_steps_cuda(tok, start_pos)
-        tok = int(toks[-1].item())
+    tok = dec.prefill_step(make_tokens(start_pos, 151936, seed=1))
     assert dec.position() == start_pos
     buf = torch.empty(steps + 1, dtype=torch.int32, device="cuda")
     buf[0] = tok
@@ -84,6 +100,30 @@ def time_bucket(dec, start_pos: int, steps: int, first_token: int):
     per_launch = sum(a.elapsed_time(b) for a, b in ev) / steps / 1e3
     dec.check()
     return wall, per_launch
+
+
+def time_prefill(dec, n: int, reps: int):
+    import torch
+    from megaqwen_amd.synthetic import make_tokens
+    toks = make_tokens(n, 151936, seed=1)
+    dec.reset()
+    dec.prefill_step(toks)                       # warm-up
+    times = []
+    for _ in range(reps):
+        dec.reset()
+        d = toks.cuda()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        rc = dec._lib.mq_prefill(dec._h, d.data_ptr(), n, dec._tok.data_ptr() + 4, None,
+                                 torch.cuda.current_stream().cuda_stream)
+        b.record()
+        if rc != 0:
+            raise RuntimeError(dec._lib.mq_last_error().decode())
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) / 1e3)
+    dec.check()
+    return min(times), sum(times) / len(times)
 
 
 def cpu_baseline(prompt_len: int = 16, gen: int = 32):
@@ -131,26 +171,25 @@ def main():
     ap.add_argument("--mode", default="persistent", choices=["persistent", "multi_kernel"])
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): this build has no "
-              "multi-GPU path; see the sharding note in DESIGN.md", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): the decode and prefill "
+              "kernels here are single-GPU; there is no multi-GPU path", file=sys.stderr)
         sys.exit(2)
 
     import torch
     K, W = int(args.steps), int(args.warmup)
     positions = (1, 128, 4096)
     max_seq = positions[-1] + K + 8
-    dec, spec = build_decoder(max_seq)
+    dec, spec = build_decoder(max_seq, max_prefill=4096)
     dec.set_mode(args.mode)
     print(f"[bench] decoder ready: mode={dec.mode} grid={dec.grid} max_seq={max_seq}", file=sys.stderr,
           flush=True)
-    first = 9707
     # warm-up (untimed)
     dec.reset()
-    dec.decode_steps_cuda(first, W)
+    dec.decode_steps_cuda(9707, W)
     torch.cuda.synchronize()
     res = {}
     for p in positions:
-        wall, per_launch = time_bucket(dec, p, K, first)
+        wall, per_launch = time_bucket(dec, p, K)
         tok_s = K / wall
         mid = p + (K - 1) / 2
         res[p] = {"tok_s": tok_s, "ms_per_token": 1e3 * wall / K,
@@ -162,6 +201,17 @@ def main():
               f"roofline {res[p]['roofline_frac_wall'] * 100:.1f}% (wall) "
               f"{res[p]['roofline_frac_kernel'] * 100:.1f}% (kernel)", file=sys.stderr, flush=True)
 
+    pf_best, pf_mean = time_prefill(dec, 512, 5)
+    pf4_best, _ = time_prefill(dec, 4096, 2)
+    prefill = {"tokens": 512, "ms": round(pf_mean * 1e3, 3), "tok_s": round(512 / pf_mean, 1),
+               "mfma_util": round(prefill_flops(512) / pf_mean / MFMA_BF16_PEAK, 4),
+               "tflops": round(prefill_flops(512) / pf_mean / 1e12, 1),
+               "ms_4096": round(pf4_best * 1e3, 2),
+               "mfma_util_4096": round(prefill_flops(4096) / pf4_best / MFMA_BF16_PEAK, 4)}
+    print(f"[bench] prefill 512: {prefill['ms']} ms, {prefill['tok_s']} tok/s, "
+          f"{prefill['tflops']} TFLOP/s = {prefill['mfma_util'] * 100:.1f}% of dense bf16 peak; "
+          f"4096: {prefill['ms_4096']} ms ({prefill['mfma_util_4096'] * 100:.1f}%)",
+          file=sys.stderr, flush=True)
     head = res[128]
     achieved = head["bytes_per_token"] / (head["kernel_us"] * 1e-6)
     cpu = None
@@ -189,7 +239,8 @@ def main():
                    "kv_heads": 8, "head_dim": 128, "decode_mode": args.mode,
                    "tok_s_by_position": {str(p): round(r["tok_s"], 2) for p, r in res.items()},
                    "roofline_frac_by_position": {str(p): round(r["roofline_frac_wall"], 4)
-                                                 for p, r in res.items()}},
+                                                 for p, r in res.items()},
+                   "prefill": prefill},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 2), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
                      "kernel": "mq_decode_persistent_kernel" if args.mode == "persistent"

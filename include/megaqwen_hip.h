@@ -146,6 +146,10 @@ int mq_decoder_check(mq_decoder* dec, void* stream);
 int mq_prefill(mq_decoder* dec, const int32_t* d_tokens, int n, int32_t* d_token_out,
                float* d_logits, void* stream);
 
+/* Debug hook: device addresses (inside the workspace) of the prefill buffers of the last
+ * prefill: out5 = {h [n,H], xn [n,H], qkv [n,Hq*D+2*Hkv*D], att [n,Hq*D], mlp [n,I]}, bf16. */
+int mq_debug_prefill_buffers(const mq_decoder* dec, void** out5);
+
 /* ---- op-level entry points (per-op microbenchmarks; layer `layer` of the decoder's model) ----
  * (a) RMSNorm + q|k|v GEMV + q/k RMSNorm + RoPE at `pos`; writes rotated q (fp32 [Hq*D]) and the
  *     K/V cache rows at `pos` (fused_decode_ldg_common.inl:131-394). */

@@ -11,6 +11,7 @@
 
 #include <new>
 #include <string>
+#include <vector>
 
 #include "../../include/megaqwen_hip.h"
 #include "mq_decode.h"
@@ -92,6 +93,7 @@ struct mq_decoder {
   size_t kv_bytes;
   char* ws;
   MqPrefillBuffers pf;
+  std::vector<MqLayerW> host_layers;
 };
 
 extern "C" {
@@ -154,11 +156,17 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   }
   hipError_t e = hipMemcpy(ws + lay.layers, host_layers, sizeof(MqLayerW) * desc->num_layers,
                            hipMemcpyHostToDevice);
-  delete[] host_layers;
-  if (e != hipSuccess) return fail(MQ_ERR_HIP, "hipMemcpy(layer table): %s", hipGetErrorString(e));
-
+  if (e != hipSuccess) {
+    delete[] host_layers;
+    return fail(MQ_ERR_HIP, "hipMemcpy(layer table): %s", hipGetErrorString(e));
+  }
   mq_decoder* dec = new (std::nothrow) mq_decoder();
-  if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "out of host memory");
+  if (dec == nullptr) {
+    delete[] host_layers;
+    return fail(MQ_ERR_INVALID_ARG, "out of host memory");
+  }
+  dec->host_layers.assign(host_layers, host_layers + desc->num_layers);
+  delete[] host_layers;
   MqDecodeParams& p = dec->p;
   memset(&p, 0, sizeof(p));
   p.layers = reinterpret_cast<const MqLayerW*>(ws + lay.layers);
@@ -323,10 +331,21 @@ int mq_prefill(mq_decoder* dec, const int32_t* d_tokens, int n, int32_t* d_token
     return fail(MQ_ERR_INVALID_ARG, "Prefill sequence length %d exceeds maximum %d", n,
                 dec->max_prefill);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int rc = mq_launch_prefill(dec->p, dec->pf, d_tokens, n, d_token_out, d_logits, dec->grid, s);
+  int rc = mq_launch_prefill(dec->p, dec->host_layers.data(), dec->pf, d_tokens, n, d_token_out,
+                             d_logits, dec->grid, s);
   if (rc != 0) return fail(MQ_ERR_HIP, "prefill launch failed (%d)", rc);
   if (mq_launch_fill_state(dec->p.st, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
   dec->pos = n;
+  return MQ_OK;
+}
+
+int mq_debug_prefill_buffers(const mq_decoder* dec, void** out5) {
+  if (dec == nullptr || out5 == nullptr) return fail(MQ_ERR_INVALID_ARG, "NULL argument");
+  out5[0] = dec->pf.h;
+  out5[1] = dec->pf.xn;
+  out5[2] = dec->pf.qkv;
+  out5[3] = dec->pf.att;
+  out5[4] = dec->pf.m;
   return MQ_OK;
 }
 

@@ -184,14 +184,22 @@ MQ_DEV void phase_finish(Epi epilogue) {
 // xn = x * rsqrt(mean(x^2) + eps) * w over the 1024 values in LDS `x`, two per thread.
 // fused_decode_ldg_common.inl:150-191 (input norm), fused_decode_ldg_mlp.inl:70-118 (post norm),
 // fused_decode_ldg_kernel.inl:103-137 (final norm).
-MQ_DEV void norm_1024(const float* x, const bf16_t* __restrict__ w, float* xn, float* red) {
+// With `round_out` the result is rounded to bf16 (the prefill path's final norm,
+// prefill_final_norm_kernel, fused_prefill_kernels.inl:655-700).
+MQ_DEV void norm_1024(const float* x, const bf16_t* __restrict__ w, float* xn, float* red,
+                      bool round_out = false) {
   const int t = tid();
   const float2 v = reinterpret_cast<const float2*>(x)[t];
   const float ss = block_sum(v.x * v.x + v.y * v.y, red);
   const float r = rsqrtf(ss * (1.0f / MQ_H) + MQ_EPS);
   const uint32_t wv = reinterpret_cast<const uint32_t*>(w)[t];
-  xn[2 * t] = v.x * r * bf16_lo(wv);
-  xn[2 * t + 1] = v.y * r * bf16_hi(wv);
+  float y0 = v.x * r * bf16_lo(wv), y1 = v.y * r * bf16_hi(wv);
+  if (round_out) {
+    y0 = round_bf16(y0);
+    y1 = round_bf16(y1);
+  }
+  xn[2 * t] = y0;
+  xn[2 * t + 1] = y1;
 }
 
 // ------------------------------------------------------------------------------ P1: q|k|v
@@ -666,10 +674,10 @@ MQ_DEV void down_publish(int wg, int G, const float* lds, float& res, Out out) {
 // is the two-kernel reference equivalent).  Ordering between a workgroup's two atomics comes
 // from waiting for the first to return; no cache-wide fences are used.
 MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int* tok_out,
-                        float* logits, int pos, bool advance_pos) {
+                        float* logits, int pos, bool advance_pos, bool round_norm = false) {
   float* xn = lds + LDS_XN;
   uint64_t* keys = reinterpret_cast<uint64_t*>(lds + LDS_KEYS);
-  norm_1024(lds + LDS_IN, p.final_norm, xn, lds + LDS_RED);
+  norm_1024(lds + LDS_IN, p.final_norm, xn, lds + LDS_RED, round_norm);
   __syncthreads();
   const int lane = lane_id(), wave = wave_id();
   float xl[16];
@@ -959,13 +967,15 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_down_kernel(MqDecodeParams p
                  [&](int r, float v) { x_out[r] = f32_to_bf16(v); });
   });
 }
-// (d) final RMSNorm + LM head + argmax of a given bf16 hidden state.
+// (d) final RMSNorm + LM head + argmax of a given bf16 hidden state; `round_norm` rounds the
+// normalised vector to bf16 first (the prefill path).
 __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, const bf16_t* x,
-                                                               int* tok_out, float* logits) {
+                                                               int* tok_out, float* logits,
+                                                               bool round_norm) {
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   phase_sync(&p.st->sync, 0, false, MQ_NOTHING,
              [&] { wave_copy_bf16_1024(lds + LDS_IN, x); });
-  lm_head_run(p, blockIdx.x, gridDim.x, lds, tok_out, logits, 0, false);
+  lm_head_run(p, blockIdx.x, gridDim.x, lds, tok_out, logits, 0, false, round_norm);
 }
 
 // ---------------------------------------------------------------------- state kernels
@@ -1094,6 +1104,12 @@ int mq_launch_op_mlp(const MqDecodeParams& p, int layer, const float* a_in, bf16
 
 int mq_launch_op_lm_head(const MqDecodeParams& p, const bf16_t* x, int* tok_out, float* logits,
                          int grid, hipStream_t stream) {
-  mq_op_lm_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, x, tok_out, logits);
+  mq_op_lm_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, x, tok_out, logits, false);
+  return launch_status();
+}
+
+int mq_launch_lm_head_bf16norm(const MqDecodeParams& p, const bf16_t* x, int* tok_out,
+                               float* logits, int grid, hipStream_t stream) {
+  mq_op_lm_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, x, tok_out, logits, true);
   return launch_status();
 }

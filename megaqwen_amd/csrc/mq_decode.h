@@ -108,3 +108,6 @@ int mq_launch_op_mlp(const MqDecodeParams& p, int layer, const float* a_in, bf16
                      int grid, hipStream_t stream);
 int mq_launch_op_lm_head(const MqDecodeParams& p, const bf16_t* x, int* tok_out, float* logits,
                          int grid, hipStream_t stream);
+// LM head over bf16(RMSNorm(x) * w_final) (the prefill path's last-token head).
+int mq_launch_lm_head_bf16norm(const MqDecodeParams& p, const bf16_t* x, int* tok_out,
+                               float* logits, int grid, hipStream_t stream);

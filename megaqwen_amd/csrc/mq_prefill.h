@@ -14,5 +14,7 @@ struct MqPrefillBuffers {
 
 size_t mq_prefill_workspace_bytes(int max_n);
 void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n);
-int mq_launch_prefill(const MqDecodeParams& p, const MqPrefillBuffers& b, const int32_t* tokens,
-                      int n, int32_t* tok_out, float* logits, int grid, hipStream_t stream);
+// `host_layers` is the host copy of the device layer table p.layers.
+int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* host_layers,
+                      const MqPrefillBuffers& b, const int32_t* tokens, int n, int32_t* tok_out,
+                      float* logits, int grid, hipStream_t stream);

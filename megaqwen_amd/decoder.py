@@ -270,6 +270,20 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
                                         self._logits.data_ptr(), _stream_ptr()))
         return int(self._tok[1].item()), self._logits.clone()
 
+    def debug_prefill_buffers(self, n: int) -> dict:
+        """Views (bf16) of the prefill buffers after a prefill of n tokens: h, xn, qkv, att, mlp
+        (the last layer's values)."""
+        ptrs = (ctypes.c_void_p * 5)()
+        _lib.check(self._lib.mq_debug_prefill_buffers(self._h, ptrs))
+        base = self._workspace.data_ptr()
+        raw = self._workspace.view(torch.uint8)
+        widths = {"h": 1024, "xn": 1024, "qkv": 4096, "att": 2048, "mlp": 3072}
+        out = {}
+        for (name, width), ptr in zip(widths.items(), ptrs):
+            off = int(ptr) - base
+            out[name] = raw[off:off + n * width * 2].view(torch.bfloat16).view(n, width)
+        return out
+
     def _chain(self, first_token_id: int, num_steps: int) -> torch.Tensor:
         if self.position() + num_steps >= self.max_seq_len:
             raise RuntimeError("decode_steps would exceed max_seq_len")
