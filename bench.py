@@ -17,7 +17,10 @@ reported too.
 
 Roofline: algorithmic bytes per token = bf16 weights streamed (1,192,101,888 B) + KV read
 (114,688 B x (pos + 1)) + KV write (114,688 B), over the per-launch duration measured with HIP
-events on the launch stream, against 8 TB/s.
+events on the launch stream, against 8 TB/s.  `traffic` is the HBM bytes per launch measured by
+two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE over `--pmc-workload`, scaled by what the
+same counters read for a 256 MiB copy), taken from the committed profile summary and reported
+only while the decode kernel sources still hash to the measured version (else null).
 
 cpu_baseline: the CPU oracle (oracle/ref_cpu.py, PyTorch fp32 restatement of the reference decode
 path) on BASELINE config 1 (16-token prompt fed through decode, then 32 greedy tokens), timed on
@@ -37,6 +40,30 @@ sys.path.insert(0, ROOT)
 HBM_PEAK = 8.0e12
 WEIGHT_BYTES = 1_192_101_888
 KV_BYTES_PER_POS = 28 * 8 * 128 * 2 * 2     # K + V, all layers, bf16
+
+
+DECODE_SOURCES = ("decode.hip", "mq_device.h", "mq_decode.h", "mq_config.h")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_persistent_qwen3_0.6b.md")
+
+
+def decode_source_sha() -> str:
+    import hashlib
+    d = os.path.join(ROOT, "megaqwen_amd", "csrc")
+    return hashlib.sha256(b"".join(open(os.path.join(d, f), "rb").read()
+                                   for f in DECODE_SOURCES)).hexdigest()[:16]
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed FETCH_SIZE / WRITE_SIZE counter passes
+    (copy-calibrated), or None when the decode sources changed since they were measured."""
+    try:
+        kv = dict(line.strip().split(": ", 1) for line in open(TRAFFIC_PROFILE)
+                  if line.startswith("    ") and ": " in line)
+    except OSError:
+        return None
+    if kv.get("source_sha") != decode_source_sha():
+        return None
+    return int(kv["traffic_bytes_per_launch"])
 
 
 def bytes_per_token(pos: int) -> int:
@@ -126,6 +153,25 @@ def time_prefill(dec, n: int, reps: int):
     return min(times), sum(times) / len(times)
 
 
+def pmc_workload():
+    """Fixed short run for counter passes (rocprofv3 --pmc ...): every dispatch is profiled, so
+    it stays small.  The 256 MiB copy is the calibration kernel for the traffic counters."""
+    import torch
+    from megaqwen_amd.synthetic import make_tokens
+    a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    dec, _ = build_decoder(256, max_prefill=128)
+    tok = dec.prefill_step(make_tokens(128, 151936, seed=1))
+    toks = dec.decode_steps_cuda(tok, 16)
+    torch.cuda.synchronize()
+    dec.check()
+    print(f"pmc workload done: 256 MiB copy, prefill 128, decode 16 -> {toks[-1].item()}")
+
+
 def cpu_baseline(prompt_len: int = 16, gen: int = 32):
     import torch
     from megaqwen_amd.rope import build_rope_tables
@@ -169,6 +215,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mode", default="persistent", choices=["persistent", "multi_kernel"])
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="short fixed workload for hardware-counter runs: a 256 MiB device copy "
+                         "(calibration of FETCH_SIZE / WRITE_SIZE), a 128-token prefill, then 16 "
+                         "decode steps at positions 128..143")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): the decode and prefill "
@@ -176,6 +226,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.pmc_workload:
+        pmc_workload()
+        return
     K, W = int(args.steps), int(args.warmup)
     positions = (1, 128, 4096)
     max_seq = positions[-1] + K + 8
@@ -242,7 +295,8 @@ def main():
                                                  for p, r in res.items()},
                    "prefill": prefill},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 2), "peak": 8000.0,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                     "traffic": measured_traffic() if args.mode == "persistent" else None,
                      "kernel": "mq_decode_persistent_kernel" if args.mode == "persistent"
                      else "mq_decode_phase_kernel (all phases)",
                      "kernel_us": round(head["kernel_us"], 2),

@@ -15,6 +15,10 @@
  *   MegakernelPrefillDecoder.prefill_step / decode_steps_cuda
  *                                       csrc/megakernel/bindings_prefill.cpp:731-833,1045-1075
  *   launch_prefill_float .............. csrc/megakernel/fused_prefill_launch.inl:71-731
+ *   launch_ldg_fill_iota / launch_ldg_find_first_eos (device token chain of decode_greedy_cuda)
+ *                                       csrc/megakernel/fused_decode_ldg_launch.inl:5-53
+ *   chat.py decode_ldg (caller-owned caches, host position per call) ... chat.py:123-321
+ *   generate.py decode_layer / lm_head_last .............. generate.py:78-138
  */
 #ifndef MEGAQWEN_HIP_H
 #define MEGAQWEN_HIP_H
@@ -64,7 +68,7 @@ typedef struct mq_model_desc {
   int num_q_heads;        /* 16 */
   int num_kv_heads;       /* 8 */
   int head_dim;           /* 128 */
-  int num_layers;         /* >= 1 */
+  int num_layers;         /* >= 0 (0: embedding -> final norm -> LM head only) */
   int vocab_size;         /* >= 1 */
   int max_seq_len;        /* KV-cache capacity in positions */
   int max_prefill_len;    /* 0 = decode only */
@@ -104,6 +108,11 @@ int mq_decoder_position(const mq_decoder* dec);
  * captured mq_decode_steps launches: the device-side position advances inside the kernels, the
  * host counter (used for bounds checks and position()) does not. */
 int mq_decoder_set_host_position(mq_decoder* dec, int pos);
+/* Moves the decode position to `pos` (0 <= pos <= max_seq_len) on the host and, in stream order,
+ * on the device; KV rows [0, pos) are kept as they are.  Replaces the host-side position that
+ * chat.py passes to every decode_ldg call (chat.py:448-470, bindings copy it to the device per
+ * launch, fused_decode_ldg_launch.inl:55-87). */
+int mq_decoder_set_position(mq_decoder* dec, int pos, void* stream);
 /* Selects MQ_MODE_PERSISTENT or MQ_MODE_MULTI_KERNEL; returns MQ_ERR_UNSUPPORTED if the device
  * cannot co-schedule the persistent grid. */
 int mq_decoder_set_mode(mq_decoder* dec, int mode);
@@ -119,7 +128,9 @@ int mq_decode_step(mq_decoder* dec, const int32_t* d_token_in, int32_t* d_token_
                    float* d_logits, void* stream);
 
 /* decode_steps_cuda (bindings_prefill.cpp:1045-1075): d_tokens[0] holds the first token;
- * step i reads d_tokens[i] and writes d_tokens[i+1], i < n.  The chain stays on the device. */
+ * step i reads d_tokens[i] and writes d_tokens[i+1], i < n.  The chain stays on the device, so
+ * it also replaces the reference's fill_iota + first-EOS helpers
+ * (fused_decode_ldg_launch.inl:5-53) that decode_greedy_cuda builds on. */
 int mq_decode_steps(mq_decoder* dec, int32_t* d_tokens, int n, void* stream);
 
 /* Debug hook (the reference's counterpart is debug_ldg_decode_cycles,
@@ -162,6 +173,12 @@ int mq_op_attention(mq_decoder* dec, int layer, const float* d_q, int cache_len,
 /* (c) x_out = bf16(W_down(silu(W_gate n) * W_up n) + a), n = RMSNorm(a) * post_ln
  *     (fused_decode_ldg_mlp.inl:70-217).  a: fp32 [H]. */
 int mq_op_mlp(mq_decoder* dec, int layer, const float* d_a, void* d_x_out_bf16, void* stream);
+/* One whole decoder layer at position `pos` (generate.py:78-110 decode_layer): bf16 hidden in ->
+ * bf16 hidden out, writing K/V cache row `pos` of `layer` and attending over rows [0, pos].
+ * Uses the decoder's workspace; does not change the decode position.  Input and output must
+ * not alias. */
+int mq_op_decode_layer(mq_decoder* dec, int layer, const void* d_x_bf16, int pos,
+                       void* d_x_out_bf16, void* stream);
 /* (d) final RMSNorm + LM head + argmax of a bf16 hidden state (fused_decode_ldg_lm.inl:6-163);
  *     d_logits may be NULL. */
 int mq_op_lm_head(mq_decoder* dec, const void* d_x_bf16, int32_t* d_token_out, float* d_logits,

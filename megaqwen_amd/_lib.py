@@ -26,9 +26,9 @@ MQ_MODE_MULTI_KERNEL = 1
 EXPORTED = (
     "mq_abi_version", "mq_last_error", "mq_workspace_bytes", "mq_kv_cache_bytes",
     "mq_decoder_create", "mq_decoder_destroy", "mq_decoder_reset", "mq_decoder_position",
-    "mq_decoder_set_host_position", "mq_decoder_set_mode", "mq_decoder_get_mode", "mq_decoder_grid", "mq_decode_step",
+    "mq_decoder_set_host_position", "mq_decoder_set_position", "mq_decoder_set_mode", "mq_decoder_get_mode", "mq_decoder_grid", "mq_decode_step",
     "mq_decode_steps", "mq_debug_decode_step_layers", "mq_debug_decode_step_timing", "mq_decoder_check", "mq_prefill", "mq_debug_prefill_buffers", "mq_op_qkv_rope", "mq_op_attention",
-    "mq_op_mlp", "mq_op_lm_head",
+    "mq_op_mlp", "mq_op_decode_layer", "mq_op_lm_head",
 )
 
 
@@ -78,6 +78,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "mq_decoder_reset": (I, [P, P]),
         "mq_decoder_position": (I, [P]),
         "mq_decoder_set_host_position": (I, [P, I]),
+        "mq_decoder_set_position": (I, [P, I, P]),
         "mq_decoder_set_mode": (I, [P, I]),
         "mq_decoder_get_mode": (I, [P]),
         "mq_decoder_grid": (I, [P]),
@@ -91,6 +92,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "mq_op_qkv_rope": (I, [P, I, P, I, P, P]),
         "mq_op_attention": (I, [P, I, P, I, P, P]),
         "mq_op_mlp": (I, [P, I, P, P, P]),
+        "mq_op_decode_layer": (I, [P, I, P, I, P, P]),
         "mq_op_lm_head": (I, [P, P, P, P, P]),
     }
     for name, (res, args) in sig.items():

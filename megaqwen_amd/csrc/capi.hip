@@ -59,7 +59,7 @@ int check_desc(const mq_model_desc* d) {
                 "the compiled Qwen3-0.6B shape (1024, 3072, 16/8, 128)",
                 d->hidden_size, d->intermediate_size, d->num_q_heads, d->num_kv_heads,
                 d->head_dim);
-  if (d->num_layers < 1 || d->num_layers > 4096)
+  if (d->num_layers < 0 || d->num_layers > 4096)
     return fail(MQ_ERR_INVALID_ARG, "num_layers %d out of range", d->num_layers);
   if (d->vocab_size < 1) return fail(MQ_ERR_INVALID_ARG, "vocab_size %d < 1", d->vocab_size);
   if (d->max_seq_len < 1) return fail(MQ_ERR_INVALID_ARG, "max_seq_len %d < 1", d->max_seq_len);
@@ -70,7 +70,8 @@ int check_desc(const mq_model_desc* d) {
   for (const void* t : top)
     if (t == nullptr || !aligned16(t))
       return fail(MQ_ERR_INVALID_ARG, "model tensors must be non-NULL and 16-byte aligned");
-  if (d->layers == nullptr) return fail(MQ_ERR_INVALID_ARG, "layers array is NULL");
+  if (d->layers == nullptr && d->num_layers > 0)
+    return fail(MQ_ERR_INVALID_ARG, "layers array is NULL");
   for (int l = 0; l < d->num_layers; ++l) {
     const void* const* f = reinterpret_cast<const void* const*>(&d->layers[l]);
     for (int i = 0; i < 11; ++i)
@@ -220,6 +221,16 @@ int mq_decoder_set_host_position(mq_decoder* dec, int pos) {
   if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "decoder is NULL");
   if (pos < 0 || pos > dec->p.max_seq)
     return fail(MQ_ERR_POSITION, "position %d outside [0, %d]", pos, dec->p.max_seq);
+  dec->pos = pos;
+  return MQ_OK;
+}
+
+int mq_decoder_set_position(mq_decoder* dec, int pos, void* stream) {
+  if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "decoder is NULL");
+  if (pos < 0 || pos > dec->p.max_seq)
+    return fail(MQ_ERR_POSITION, "position %d outside [0, %d]", pos, dec->p.max_seq);
+  if (mq_launch_fill_state(dec->p.st, pos, static_cast<hipStream_t>(stream)) != 0)
+    return fail(MQ_ERR_HIP, "state update failed");
   dec->pos = pos;
   return MQ_OK;
 }
@@ -378,6 +389,22 @@ int mq_op_mlp(mq_decoder* dec, int layer, const float* d_a, void* d_x_out_bf16, 
     return fail(MQ_ERR_INVALID_ARG, "layer %d out of range", layer);
   int rc = mq_launch_op_mlp(dec->p, layer, d_a, static_cast<bf16_t*>(d_x_out_bf16), dec->grid,
                             static_cast<hipStream_t>(stream));
+  return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%d)", rc);
+}
+
+int mq_op_decode_layer(mq_decoder* dec, int layer, const void* d_x_bf16, int pos,
+                       void* d_x_out_bf16, void* stream) {
+  if (dec == nullptr || d_x_bf16 == nullptr || d_x_out_bf16 == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "NULL argument");
+  if (layer < 0 || layer >= dec->p.num_layers)
+    return fail(MQ_ERR_INVALID_ARG, "layer %d out of range", layer);
+  if (pos < 0 || pos >= dec->p.max_seq)
+    return fail(MQ_ERR_POSITION, "position %d outside [0, max_seq_len=%d)", pos, dec->p.max_seq);
+  if (d_x_bf16 == d_x_out_bf16)
+    return fail(MQ_ERR_INVALID_ARG, "layer input and output must not alias");
+  int rc = mq_launch_op_layer(dec->p, layer, static_cast<const bf16_t*>(d_x_bf16), pos,
+                              static_cast<bf16_t*>(d_x_out_bf16), dec->grid,
+                              static_cast<hipStream_t>(stream));
   return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%d)", rc);
 }
 

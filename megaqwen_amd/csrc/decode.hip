@@ -786,7 +786,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
   GateUpSet wgu;
   DownSet wd;
   KvBlock kv;
-  qkv_load(wq, p.layers[0], wg, G);
+  if (p.num_layers > 0) qkv_load(wq, p.layers[0], wg, G);
   phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_bf16_1024(lds + LDS_IN, xe); });
   for (int l = 0; l < p.num_layers; ++l) {
     const MqLayerW w = p.layers[l];
@@ -845,7 +845,10 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
   row_range(MQ_H, wg, G, r0h, nrh);
   const int t = lane_id();
   if constexpr (PH == 5) {
-    phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, s->hidden); });
+    phase_sync(sy, 0, false, MQ_NOTHING, [&] {
+      if (p.num_layers == 0) wave_copy_bf16_1024(lds + LDS_IN, xe);
+      else wave_copy_coh<MQ_H>(lds + LDS_IN, s->hidden);
+    });
     lm_head_run(p, wg, G, lds, p.tok_out, p.logits, pos, true);
   } else {
     const MqLayerW w = p.layers[l];
@@ -940,6 +943,21 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_merge_kernel(MqDecodeParams 
                                                                   float* att_out) {
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   attn_merge_head(p.s->part, blockIdx.x, nch, att_out, lds);
+}
+// O projection with residual: a_out = W_o att + x (x bf16, the layer input).
+__global__ void __launch_bounds__(MQ_THREADS) mq_op_o_kernel(MqDecodeParams p, int l,
+                                                              const float* att, const bf16_t* x,
+                                                              float* a_out) {
+  __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
+  OSet ws;
+  o_load(ws, p.layers[l], blockIdx.x, gridDim.x);
+  int r0, nr;
+  row_range(MQ_H, blockIdx.x, gridDim.x, r0, nr);
+  float res = lane_id() < nr ? bf16_to_f32(x[r0 + lane_id()]) : 0.f;
+  phase_sync(&p.st->sync, 0, false, MQ_NOTHING,
+             [&] { wave_copy_coh<MQ_QDIM>(lds + LDS_IN, att); });
+  o_run(ws, p.layers[l], blockIdx.x, gridDim.x, lds);
+  phase_finish([&] { o_publish(a_out, blockIdx.x, gridDim.x, lds, res); });
 }
 // (c) SwiGLU MLP with residual: x_out = bf16(W_d (silu(W_g n) * W_u n) + a), n = RMSNorm(a).
 __global__ void __launch_bounds__(MQ_THREADS) mq_op_gateup_kernel(MqDecodeParams p, int l,
@@ -1099,6 +1117,21 @@ int mq_launch_op_mlp(const MqDecodeParams& p, int layer, const float* a_in, bf16
                      int grid, hipStream_t stream) {
   mq_op_gateup_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, layer, a_in);
   mq_op_down_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, layer, a_in, x_out);
+  return launch_status();
+}
+
+int mq_launch_op_layer(const MqDecodeParams& p, int layer, const bf16_t* x, int pos,
+                       bf16_t* x_out, int grid, hipStream_t stream) {
+  // Scratch use: q_hat -> s->mlp (free until gate/up), attention -> s->att, O output -> s->a.
+  MqScratch* s = p.s;
+  const int nch = mq_attn_nchunks(pos + 1, grid);
+  mq_op_qkv_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, layer, x);
+  mq_op_rope_kernel<<<MQ_NKV, MQ_THREADS, 0, stream>>>(p, layer, pos, s->mlp);
+  mq_op_attn_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, layer, s->mlp, pos + 1, nch);
+  mq_op_merge_kernel<<<MQ_NKV, MQ_THREADS, 0, stream>>>(p, nch, s->att);
+  mq_op_o_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, layer, s->att, x, s->a);
+  mq_op_gateup_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, layer, s->a);
+  mq_op_down_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, layer, s->a, x_out);
   return launch_status();
 }
 

@@ -106,6 +106,8 @@ int mq_launch_op_attention(const MqDecodeParams& p, int layer, const float* q_ha
                            float* att_out, int grid, hipStream_t stream);
 int mq_launch_op_mlp(const MqDecodeParams& p, int layer, const float* a_in, bf16_t* x_out,
                      int grid, hipStream_t stream);
+int mq_launch_op_layer(const MqDecodeParams& p, int layer, const bf16_t* x, int pos,
+                       bf16_t* x_out, int grid, hipStream_t stream);
 int mq_launch_op_lm_head(const MqDecodeParams& p, const bf16_t* x, int* tok_out, float* logits,
                          int grid, hipStream_t stream);
 // LM head over bf16(RMSNorm(x) * w_final) (the prefill path's last-token head).

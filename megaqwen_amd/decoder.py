@@ -45,7 +45,8 @@ class MegakernelDecoder:
     """Batch-1 greedy decoder (bindings_decode.cpp:80-280) over the HIP decode kernels."""
 
     def __init__(self, embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight,
-                 cos_table, sin_table, num_layers, max_seq_len, max_prefill_len=0):
+                 cos_table, sin_table, num_layers, max_seq_len, max_prefill_len=0, *,
+                 k_cache=None, v_cache=None):
         lib = _lib.load()
         self._lib = lib
         num_layers, max_seq_len = int(num_layers), int(max_seq_len)
@@ -71,10 +72,16 @@ class MegakernelDecoder:
             ptrs = [t.data_ptr() for t in self.layer_weights[11 * l:11 * (l + 1)]]
             layers[l] = _lib.LayerWeights(*ptrs)
         w = self.layer_weights
+        if num_layers > 0:
+            shape = dict(intermediate_size=int(w[8].shape[0]),
+                         num_q_heads=int(w[1].shape[0]) // int(w[4].shape[0]),
+                         num_kv_heads=int(w[2].shape[0]) // int(w[5].shape[0]),
+                         head_dim=int(w[4].shape[0]))
+        else:
+            shape = {k: COMPILED_LAYER_SHAPE[k] for k in
+                     ("intermediate_size", "num_q_heads", "num_kv_heads", "head_dim")}
         self._desc = _lib.ModelDesc(
-            hidden_size=int(hidden), intermediate_size=int(w[8].shape[0]),
-            num_q_heads=int(w[1].shape[0]) // int(w[4].shape[0]),
-            num_kv_heads=int(w[2].shape[0]) // int(w[5].shape[0]), head_dim=int(w[4].shape[0]),
+            hidden_size=int(hidden), **shape,
             num_layers=num_layers, vocab_size=int(vocab), max_seq_len=max_seq_len,
             max_prefill_len=self.max_prefill_len, embed=self.embed_weight.data_ptr(),
             final_norm=self.final_norm_weight.data_ptr(), lm_head=self.lm_head_weight.data_ptr(),
@@ -84,8 +91,21 @@ class MegakernelDecoder:
         ws_bytes = lib.mq_workspace_bytes(ctypes.byref(self._desc))
         if ws_bytes == 0:
             raise _lib.MegaQwenError(_lib.MQ_ERR_INVALID_ARG, lib.mq_last_error().decode())
-        self.k_cache = torch.zeros(num_layers, _NKV, max_seq_len, _D, dtype=torch.bfloat16, device=device)
-        self.v_cache = torch.zeros_like(self.k_cache)
+        cache_shape = (max(num_layers, 1), _NKV, max_seq_len, _D)
+        if (k_cache is None) != (v_cache is None):
+            raise ValueError("pass both k_cache and v_cache, or neither")
+        if k_cache is None:
+            self.k_cache = torch.zeros(cache_shape, dtype=torch.bfloat16, device=device)
+            self.v_cache = torch.zeros_like(self.k_cache)
+        else:
+            # caller-owned caches (chat.py:409-421): [layers, kv_heads, max_seq_len, head_dim]
+            for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+                if (not isinstance(c, torch.Tensor) or not c.is_cuda or c.dtype != torch.bfloat16
+                        or not c.is_contiguous() or c.numel() < num_layers * _NKV * max_seq_len * _D
+                        or c.shape[-2:] != (max_seq_len, _D)):
+                    raise ValueError(f"{name} must be a contiguous bf16 CUDA tensor of shape "
+                                     f"[{num_layers}, {_NKV}, {max_seq_len}, {_D}]")
+            self.k_cache, self.v_cache = k_cache, v_cache
         self._workspace = torch.zeros((ws_bytes + 255) // 256 * 64, dtype=torch.int32, device=device)
         assert self._workspace.data_ptr() % 256 == 0
         self._tok = torch.zeros(2, dtype=torch.int32, device=device)
@@ -150,6 +170,11 @@ class MegakernelDecoder:
             _stream_ptr()))
         return int(self._tok[1].item()), stamps
 
+    def set_position(self, position: int) -> None:
+        """Moves the decode position (host and device) without touching the KV cache; the
+        chat.py binding passes the position with every call (chat.py:448-470)."""
+        _lib.check(self._lib.mq_decoder_set_position(self._h, int(position), _stream_ptr()))
+
     def reset(self) -> None:
         """Zeroes the KV cache and sets the position to 0 (bindings_decode.cpp:236-240)."""
         _lib.check(self._lib.mq_decoder_reset(self._h, _stream_ptr()))
@@ -208,6 +233,19 @@ class MegakernelDecoder:
             x_out = torch.empty(a.numel(), dtype=torch.bfloat16, device=a.device)
         _lib.check(self._lib.mq_op_mlp(self._h, int(layer), a.contiguous().data_ptr(),
                                        x_out.data_ptr(), _stream_ptr()))
+        return x_out
+
+    def op_decode_layer(self, layer: int, x: torch.Tensor, pos: int,
+                        x_out: torch.Tensor | None = None) -> torch.Tensor:
+        """One decoder layer at `pos` (generate.py:78-110): bf16 [1024] in -> bf16 [1024] out;
+        writes KV row `pos` of `layer`, attends over rows [0, pos]."""
+        x = _bf16_cuda(x, "x").reshape(-1)
+        if x.numel() != 1024:
+            raise ValueError("x must hold 1024 elements")
+        if x_out is None:
+            x_out = torch.empty_like(x)
+        _lib.check(self._lib.mq_op_decode_layer(self._h, int(layer), x.data_ptr(), int(pos),
+                                                x_out.data_ptr(), _stream_ptr()))
         return x_out
 
     def op_lm_head(self, x: torch.Tensor, tok_out: torch.Tensor | None = None,
