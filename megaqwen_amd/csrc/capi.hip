@@ -59,7 +59,7 @@ int check_desc(const mq_model_desc* d) {
                 "the compiled Qwen3-0.6B shape (1024, 3072, 16/8, 128)",
                 d->hidden_size, d->intermediate_size, d->num_q_heads, d->num_kv_heads,
                 d->head_dim);
-  if (d->num_layers < 0 || d->num_layers > 4096)
+  if (d->num_layers < 0 || d->num_layers > MQ_MAX_LAYERS)
     return fail(MQ_ERR_INVALID_ARG, "num_layers %d out of range", d->num_layers);
   if (d->vocab_size < 1) return fail(MQ_ERR_INVALID_ARG, "vocab_size %d < 1", d->vocab_size);
   if (d->max_seq_len < 1) return fail(MQ_ERR_INVALID_ARG, "max_seq_len %d < 1", d->max_seq_len);

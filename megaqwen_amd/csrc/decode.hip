@@ -50,7 +50,10 @@ static_assert(MQ_SYNC_WAVE == MQ_CWAVES && MQ_CWAVES + 1 == MQ_WAVES, "one sync 
 #define LDS_PR 4096       // [256]  per-item partial dot products
 #define LDS_RED 4352      // [16]   block reductions
 #define LDS_KEYS 4368     // [16]   8 argmax keys (u64)
-#define MQ_LDS_FLOATS 4608
+#define LDS_HID 4608      // [1024] the layer input (residual of the attention block)
+#define LDS_A 5632        // [1024] a = layer input + attention block output (MLP residual)
+#define LDS_ATTH 0        // [256]  merged attention output of the group's two query heads
+#define MQ_LDS_FLOATS 6656
 
 // Balanced contiguous row range of workgroup `wg` out of `G` for an `n`-row matrix.
 MQ_DEV void row_range(int n, int wg, int G, int& r0, int& nr) {
@@ -228,83 +231,98 @@ MQ_DEV void qkv_publish(float* qkv, int wg, int G, const float* lds) {
 // LDS carve of the attention phase (floats).
 #define ALDS_RAW 0        // [512] raw q(2 heads) | k | v of this kv head (sync wave input)
 #define ALDS_QS 512       // [256] rotated q of the two query heads
-#define ALDS_KN 768       // [128] new-position k (bf16 values)
+#define ALDS_KN 768       // [128] new-position k-hat (bf16 values)
 #define ALDS_VN 896       // [128] new-position v (bf16 values)
-#define ALDS_SC 1024      // [2][MQ_ATT_BLOCK] scores / probabilities
-#define ALDS_STAT (ALDS_SC + 2 * MQ_ATT_BLOCK)   // m[2], l[2], alpha[2]
-#define ALDS_ORED (ALDS_STAT + 16)               // [MQ_CWAVES][256] per-wave partial outputs
-// The merge runs after this item's partial has been published, so it reuses the score area.
-#define ALDS_MW ALDS_SC                          // merge: (m, l)[2][64] then weights [2][64]
+#define ALDS_PRM 1024     // [512] q_norm | k_norm | cos row | sin row of this step, as fp32
+#define ALDS_WML 1536     // [MQ_CWAVES][4] per-wave m0, m1, l0, l1
+#define ALDS_STAT 1568    // m[2], l[2] of the item
+#define ALDS_ORED 1584    // [MQ_CWAVES][256] per-wave unnormalised outputs; the item's in [0, 256)
+#define ALDS_WSC (ALDS_ORED + MQ_CWAVES * 256)   // [MQ_CWAVES][2][32] each wave's scores
+// The merge of several chunks runs after this item's partial has been published and after the
+// prologue's parameters have been used, so it reuses the parameter area.
+#define ALDS_MW ALDS_PRM                         // merge: (m, l)[2][64] then weights [2][64]
 #define ALDS_MSUM (ALDS_MW + 512)                // merge: [4][2][128] partial sums
-static_assert(ALDS_ORED + MQ_CWAVES * 256 <= MQ_LDS_FLOATS, "attention LDS carve");
+static_assert(ALDS_WSC + MQ_CWAVES * 64 <= MQ_LDS_FLOATS, "attention LDS carve");
 static_assert(ALDS_MSUM + 1024 <= MQ_LDS_FLOATS, "attention merge LDS carve");
+static_assert(ALDS_MSUM + 1024 <= ALDS_ORED + MQ_CWAVES * 256, "merge stays in the phase carve");
 
 // q/k RMSNorm over one head held as (lane, lane + 64) of one wave, then rotate-half RoPE with
 // the bf16 table row (fused_decode_ldg_common.inl:268-394):
 //   o_i = x_i c_i - x_{i+64} s_i,  o_{i+64} = x_i s_{i+64} + x_{i+64} c_{i+64}.
-MQ_DEV void head_norm_rope(float& lo, float& hi, const bf16_t* __restrict__ nw,
-                           const bf16_t* __restrict__ cs, const bf16_t* __restrict__ sn) {
+// nw, cs, sn: norm weight, cos row and sin row as fp32 in LDS.
+MQ_DEV void head_norm_rope(float& lo, float& hi, const float* nw, const float* cs,
+                           const float* sn) {
   const int lane = lane_id();
   const float ss = wave_sum(lo * lo + hi * hi);
   const float r = rsqrtf(ss * (1.0f / MQ_D) + MQ_EPS);
-  const float a = lo * r * bf16_to_f32(nw[lane]);
-  const float b = hi * r * bf16_to_f32(nw[lane + 64]);
-  const float c_lo = bf16_to_f32(cs[lane]), c_hi = bf16_to_f32(cs[lane + 64]);
-  const float s_lo = bf16_to_f32(sn[lane]), s_hi = bf16_to_f32(sn[lane + 64]);
-  lo = a * c_lo - b * s_lo;
-  hi = a * s_hi + b * c_hi;
+  const float a = lo * r * nw[lane];
+  const float b = hi * r * nw[lane + 64];
+  lo = a * cs[lane] - b * sn[lane];
+  hi = a * sn[lane + 64] + b * cs[lane + 64];
 }
 
 MQ_DEV float* part_ptr(float* part, int h, int c, int j) {
   return part + ((size_t)(h * MQ_MAX_CHUNKS + c) * MQ_GQA + j) * MQ_PART_STRIDE;
 }
 
-// Sync-wave input of an attention item: raw q of query heads 2h, 2h+1, k and v of kv head h.
-MQ_DEV void attn_input(const float* qkv, int h, float* lds) {
+// Sync-wave input of an attention item, one memory round trip: raw q of query heads 2h, 2h+1,
+// k and v of kv head h (coherent loads of the q|k|v vector), plus the read-only parameters of the
+// prologue (q_norm and k_norm weights of the layer, RoPE table rows of the position).
+MQ_DEV void attn_input(const float* qkv, const bf16_t* qn, const bf16_t* kn, const bf16_t* cs,
+                       const bf16_t* sn, int h, float* lds) {
   const int lane = lane_id();
   float2 v[4];
   v[0] = ld_coh2(qkv + 2 * h * MQ_D + 2 * lane);
   v[1] = ld_coh2(qkv + 2 * h * MQ_D + 128 + 2 * lane);
   v[2] = ld_coh2(qkv + MQ_QDIM + h * MQ_D + 2 * lane);
   v[3] = ld_coh2(qkv + MQ_QDIM + MQ_KVDIM + h * MQ_D + 2 * lane);
+  uint32_t prm[4];
+  prm[0] = reinterpret_cast<const uint32_t*>(qn)[lane];
+  prm[1] = reinterpret_cast<const uint32_t*>(kn)[lane];
+  prm[2] = reinterpret_cast<const uint32_t*>(cs)[lane];
+  prm[3] = reinterpret_cast<const uint32_t*>(sn)[lane];
 #pragma unroll
   for (int i = 0; i < 4; ++i) reinterpret_cast<float2*>(lds + ALDS_RAW)[lane + 64 * i] = v[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    reinterpret_cast<float2*>(lds + ALDS_PRM)[64 * i + lane] =
+        make_float2(bf16_lo(prm[i]), bf16_hi(prm[i]));
 }
 
-// Prologue of an attention item for kv head h at decode position `pos` (raw inputs in LDS):
-// q-hat of query heads 2h, 2h+1; k-hat and v of the new position rounded to bf16 (kept as fp32)
-// and, when `write_cache`, stored into the cache row `pos`.  Waves 0..3 each own one head.
-MQ_DEV void attn_prologue(const MqDecodeParams& p, int layer, const MqLayerW& w, int h, int pos,
-                          bool write_cache, float* lds) {
+// Prologue of an attention item (inputs and parameters in LDS): q-hat of query heads 2h, 2h+1
+// into ALDS_QS; k-hat and v of the new position rounded to bf16 (kept as fp32) into
+// ALDS_KN / ALDS_VN.  Waves 0..3 each own one head.  The cache row itself is written later by
+// the sync wave (attn_cache_row), so no compute wave ever waits for a store.
+MQ_DEV void attn_prologue(float* lds) {
   const int lane = lane_id(), wave = wave_id();
   const float* raw = lds + ALDS_RAW;
-  const bf16_t* cs = p.cos + (size_t)pos * MQ_D;
-  const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
-  const size_t row = (((size_t)layer * MQ_NKV + h) * p.max_seq + pos) * MQ_D;
+  const float* prm = lds + ALDS_PRM;
   if (wave < 2) {
     float lo = raw[wave * MQ_D + lane], hi = raw[wave * MQ_D + 64 + lane];
-    head_norm_rope(lo, hi, w.q_norm, cs, sn);
+    head_norm_rope(lo, hi, prm, prm + 256, prm + 384);
     lds[ALDS_QS + wave * MQ_D + lane] = lo;
     lds[ALDS_QS + wave * MQ_D + 64 + lane] = hi;
   } else if (wave == 2) {
     float lo = raw[256 + lane], hi = raw[256 + 64 + lane];
-    head_norm_rope(lo, hi, w.k_norm, cs, sn);
-    const bf16_t blo = f32_to_bf16(lo), bhi = f32_to_bf16(hi);
-    lds[ALDS_KN + lane] = bf16_to_f32(blo);
-    lds[ALDS_KN + 64 + lane] = bf16_to_f32(bhi);
-    if (write_cache) {
-      p.kc[row + lane] = blo;
-      p.kc[row + 64 + lane] = bhi;
-    }
+    head_norm_rope(lo, hi, prm + 128, prm + 256, prm + 384);
+    lds[ALDS_KN + lane] = round_bf16(lo);
+    lds[ALDS_KN + 64 + lane] = round_bf16(hi);
   } else if (wave == 3) {
-    const bf16_t blo = f32_to_bf16(raw[384 + lane]), bhi = f32_to_bf16(raw[384 + 64 + lane]);
-    lds[ALDS_VN + lane] = bf16_to_f32(blo);
-    lds[ALDS_VN + 64 + lane] = bf16_to_f32(bhi);
-    if (write_cache) {
-      p.vc[row + lane] = blo;
-      p.vc[row + 64 + lane] = bhi;
-    }
+    lds[ALDS_VN + lane] = round_bf16(raw[384 + lane]);
+    lds[ALDS_VN + 64 + lane] = round_bf16(raw[384 + 64 + lane]);
   }
+}
+
+// Sync wave: the new position's K and V rows (bf16) into the cache of `layer`, kv head h.
+MQ_DEV void attn_cache_row(const MqDecodeParams& p, int layer, int h, int pos, const float* lds) {
+  const int lane = lane_id();
+  const size_t row = (((size_t)layer * MQ_NKV + h) * p.max_seq + pos) * MQ_D;
+  const uint32_t k2 = (uint32_t)f32_to_bf16(lds[ALDS_KN + 2 * lane]) |
+                      ((uint32_t)f32_to_bf16(lds[ALDS_KN + 2 * lane + 1]) << 16);
+  const uint32_t v2 = (uint32_t)f32_to_bf16(lds[ALDS_VN + 2 * lane]) |
+                      ((uint32_t)f32_to_bf16(lds[ALDS_VN + 2 * lane + 1]) << 16);
+  reinterpret_cast<uint32_t*>(p.kc + row)[lane] = k2;
+  reinterpret_cast<uint32_t*>(p.vc + row)[lane] = v2;
 }
 
 // K/V of up to MQ_ATT_BLOCK positions: position blk + k*28 + wave*4 + (lane/16) goes to compute
@@ -330,97 +348,89 @@ MQ_DEV const bf16_t* kv_base(const bf16_t* cache, const MqDecodeParams& p, int l
   return cache + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D + (lane_id() & 15) * 8;
 }
 
-MQ_DEV void attn_stat_init(float* lds) {
-  if (tid() < 2) {
-    lds[ALDS_STAT + tid()] = -INFINITY;
-    lds[ALDS_STAT + 2 + tid()] = 0.f;
-  }
-}
-
 // Core of one attention item: kv head h, cache positions [p0, p1), first block already in `b`.
 // Rotated queries in ALDS_QS; position `pos_new` (if inside the range) takes its K/V from
-// ALDS_KN/ALDS_VN instead of the cache.  Per block: q.K for 4 positions per wave-instruction
-// (16 lanes x 8 dims, DPP row sums), max/exp pass in LDS, p * V accumulated in registers; blocks
-// are merged with the running max.  Leaves m[2], l[2] in ALDS_STAT and the unnormalised o[2][128]
-// in ALDS_ORED[0..255] (reference: fused_decode_ldg_common.inl:417-602; split-K precedent
-// split_decode_gemm.cu:748-904).
+// ALDS_KN/ALDS_VN instead of the cache.  Each compute wave runs its own online softmax over its
+// positions (4 per wave-instruction: 16 lanes x 8 dims, DPP row sums), keeping scores, running
+// max, sum and p * V in registers; one merge over the waves at the end.  Leaves m[2], l[2] in
+// ALDS_STAT and the unnormalised o[2][128] in ALDS_ORED[0..255] (reference:
+// fused_decode_ldg_common.inl:417-602).
 MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1, int pos_new,
                       KvBlock& b, float* lds) {
   const float* qs = lds + ALDS_QS;
   const float* kn = lds + ALDS_KN;
   const float* vn = lds + ALDS_VN;
-  float* sc = lds + ALDS_SC;
+  float* wml = lds + ALDS_WML;
   float* stat = lds + ALDS_STAT;
   float* ored = lds + ALDS_ORED;
   const int lane = lane_id(), wave = wave_id();
-  const bool cw = wave < MQ_CWAVES;
   const int g = lane >> 4, sub = lane & 15;
-  const bf16_t* Kb = kv_base(p.kc, p, layer, h);
-  const bf16_t* Vb = kv_base(p.vc, p, layer, h);
-
-  float q0[8], q1[8];
+  if (wave < MQ_CWAVES) {
+    const bf16_t* Kb = kv_base(p.kc, p, layer, h);
+    const bf16_t* Vb = kv_base(p.vc, p, layer, h);
+    float q0[8], q1[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    q0[e] = qs[sub * 8 + e];
-    q1[e] = qs[MQ_D + sub * 8 + e];
-  }
-  float acc0[8], acc1[8];
+    for (int e = 0; e < 8; ++e) {
+      q0[e] = qs[sub * 8 + e];
+      q1[e] = qs[MQ_D + sub * 8 + e];
+    }
+    float acc0[8], acc1[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc0[e] = acc1[e] = 0.f;
-
-  for (int blk = p0; blk < p1; blk += MQ_ATT_BLOCK) {
-    const int bend = min(p1, blk + MQ_ATT_BLOCK);
-    if (blk != p0) kv_block_load(b, Kb, Vb, blk, bend);
-    if (cw) {
+    for (int e = 0; e < 8; ++e) acc0[e] = acc1[e] = 0.f;
+    float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;   // l: this lane's row only
+    for (int blk = p0; blk < p1; blk += MQ_ATT_BLOCK) {
+      // keeps the next block's loads from being hoisted into this one (two blocks would not
+      // fit in registers)
+      asm volatile("" ::: "memory");
+      const int bend = min(p1, blk + MQ_ATT_BLOCK);
+      if (blk != p0) kv_block_load(b, Kb, Vb, blk, bend);
+      if (pos_new >= blk && pos_new < bend) {
+        // the new position is not in the cache yet: its bf16 K/V (exact as bf16) replace the
+        // registers of the lane row that holds it
+        const uint4 knp = pack8_bf16(kn + sub * 8), vnp = pack8_bf16(vn + sub * 8);
+#pragma unroll
+        for (int k = 0; k < MQ_ATT_NK; ++k) {
+          if (blk + k * 4 * MQ_CWAVES + wave * 4 + g == pos_new) {
+            b.k[k] = knp;
+            b.v[k] = vnp;
+          }
+        }
+      }
+      // scores of this wave's 32 positions, (head, k * 4 + row), in its own LDS slice
+      float* wsc = lds + ALDS_WSC + wave * 64;
+      float mx0 = -INFINITY, mx1 = -INFINITY;
+      // position slots k of this wave holding at least one position below bend (wave-uniform)
+      const int nk = min(MQ_ATT_NK, max(0, (bend - blk - wave * 4 + 4 * MQ_CWAVES - 1) /
+                                               (4 * MQ_CWAVES)));
 #pragma unroll
       for (int k = 0; k < MQ_ATT_NK; ++k) {
+        if (k >= nk) break;
         const int pp = blk + k * 4 * MQ_CWAVES + wave * 4 + g;
         float kv[8];
         unpack8(b.k[k], kv);
-        if (pp == pos_new) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) kv[e] = kn[sub * 8 + e];
-        }
-        float s0 = 0.f, s1 = 0.f;
+        float d0 = 0.f, d1 = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          s0 = fmaf(q0[e], kv[e], s0);
-          s1 = fmaf(q1[e], kv[e], s1);
+          d0 = fmaf(q0[e], kv[e], d0);
+          d1 = fmaf(q1[e], kv[e], d1);
         }
-        s0 = row16_sum(s0);
-        s1 = row16_sum(s1);
-        if (pp < bend && sub == 0) {
-          sc[pp - blk] = s0 * p.scale_log2;
-          sc[MQ_ATT_BLOCK + pp - blk] = s1 * p.scale_log2;
+        d0 = pp < bend ? row16_sum(d0) * p.scale_log2 : -INFINITY;
+        d1 = pp < bend ? row16_sum(d1) * p.scale_log2 : -INFINITY;
+        if (sub == 0) {
+          wsc[k * 4 + g] = d0;
+          wsc[32 + k * 4 + g] = d1;
         }
+        mx0 = fmaxf(mx0, d0);
+        mx1 = fmaxf(mx1, d1);
       }
-    }
-    __syncthreads();
-    if (wave < 2) {
-      float* s = sc + wave * MQ_ATT_BLOCK;
-      const int nb = bend - blk;
-      float mx = -INFINITY;
-      for (int i = lane; i < nb; i += 64) mx = fmaxf(mx, s[i]);
-      mx = wave_max(mx);
-      const float m_old = stat[wave];
-      const float m_new = fmaxf(m_old, mx);
-      const float alpha = exp2f(m_old - m_new);
-      float ls = 0.f;
-      for (int i = lane; i < nb; i += 64) {
-        const float e = exp2f(s[i] - m_new);
-        s[i] = e;
-        ls += e;
-      }
-      ls = wave_sum(ls);
-      if (lane == 0) {
-        stat[wave] = m_new;
-        stat[2 + wave] = stat[2 + wave] * alpha + ls;
-        stat[4 + wave] = alpha;
-      }
-    }
-    __syncthreads();
-    if (cw) {
-      const float al0 = stat[4], al1 = stat[5];
+      mx0 = max_xor32(max_xor16(mx0));
+      mx1 = max_xor32(max_xor16(mx1));
+      const float n0 = fmaxf(m0, mx0), n1 = fmaxf(m1, mx1);
+      // rescale of what this wave accumulated so far (nothing yet while its max is -inf)
+      const float al0 = n0 == -INFINITY ? 1.f : exp2f(m0 - n0);
+      const float al1 = n1 == -INFINITY ? 1.f : exp2f(m1 - n1);
+      l0 *= al0;
+      l1 *= al1;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         acc0[e] *= al0;
@@ -428,34 +438,31 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
       }
 #pragma unroll
       for (int k = 0; k < MQ_ATT_NK; ++k) {
+        if (k >= nk) break;
         const int pp = blk + k * 4 * MQ_CWAVES + wave * 4 + g;
-        if (pp < bend) {
-          float vv[8];
-          unpack8(b.v[k], vv);
-          if (pp == pos_new) {
+        const float w0 = pp < bend ? exp2f(wsc[k * 4 + g] - n0) : 0.f;
+        const float w1 = pp < bend ? exp2f(wsc[32 + k * 4 + g] - n1) : 0.f;
+        l0 += w0;
+        l1 += w1;
+        float vv[8];
+        unpack8(b.v[k], vv);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vv[e] = vn[sub * 8 + e];
-          }
-          const float w0 = sc[pp - blk], w1 = sc[MQ_ATT_BLOCK + pp - blk];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            acc0[e] = fmaf(w0, vv[e], acc0[e]);
-            acc1[e] = fmaf(w1, vv[e], acc1[e]);
-          }
+        for (int e = 0; e < 8; ++e) {
+          acc0[e] = fmaf(w0, vv[e], acc0[e]);
+          acc1[e] = fmaf(w1, vv[e], acc1[e]);
         }
       }
+      m0 = n0;
+      m1 = n1;
     }
-    __syncthreads();
-  }
-  // reduce the 4 position rows of each compute wave, then the compute waves
-  if (cw) {
+    // sum the wave's 4 position rows
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      acc0[e] += xor_lane(acc0[e], 16);
-      acc0[e] += xor_lane(acc0[e], 32);
-      acc1[e] += xor_lane(acc1[e], 16);
-      acc1[e] += xor_lane(acc1[e], 32);
+      acc0[e] = sum_xor32(sum_xor16(acc0[e]));
+      acc1[e] = sum_xor32(sum_xor16(acc1[e]));
     }
+    l0 = sum_xor32(sum_xor16(l0));
+    l1 = sum_xor32(sum_xor16(l1));
     if (g == 0) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -463,13 +470,33 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
         ored[wave * 256 + MQ_D + sub * 8 + e] = acc1[e];
       }
     }
+    if (lane == 0) {
+      wml[wave * 4 + 0] = m0;
+      wml[wave * 4 + 1] = m1;
+      wml[wave * 4 + 2] = l0;
+      wml[wave * 4 + 3] = l1;
+    }
   }
   __syncthreads();
+  // merge the compute waves (every item has at least one valid position, so M is finite)
   if (tid() < 256) {
-    float o = 0.f;
+    const int j = tid() >> 7;
+    float M = -INFINITY;
 #pragma unroll
-    for (int w8 = 0; w8 < MQ_CWAVES; ++w8) o += ored[w8 * 256 + tid()];
+    for (int w8 = 0; w8 < MQ_CWAVES; ++w8) M = fmaxf(M, wml[w8 * 4 + j]);
+    float o = 0.f, L = 0.f;
+#pragma unroll
+    for (int w8 = 0; w8 < MQ_CWAVES; ++w8) {
+      const float mw = wml[w8 * 4 + j];
+      const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
+      o = fmaf(f, ored[w8 * 256 + tid()], o);
+      L = fmaf(f, wml[w8 * 4 + 2 + j], L);
+    }
     ored[tid()] = o;   // each thread rewrites only the slot it alone read last
+    if ((tid() & 127) == 0) {
+      stat[j] = M;
+      stat[2 + j] = L;
+    }
   }
   __syncthreads();
 }
@@ -491,21 +518,23 @@ MQ_DEV void attn_write_partial(float* part, int h, int c, const float* lds) {
 // by all 512 threads with every load issued up front (one memory round trip):
 //   att_j = sum_c exp2(m_c - M_j) o_c / sum_c exp2(m_c - M_j) l_c.
 // Thread t owns query head j = t / 256, dims 2*((t / 4) % 64) + {0, 1} and chunks c = t % 4 + 4i.
-MQ_DEV void attn_merge_head(const float* part, int h, int nch, float* att, float* lds) {
+template <class Out>
+MQ_DEV void attn_merge(const float* part, int h, int nch, float* lds, Out out) {
   float* mw = lds + ALDS_MW;      // (m, l) pairs [2][64] -> weights [2][64] at +256
   float* msum = lds + ALDS_MSUM;  // [4][2][128]
   const int t = tid();
   const int j = t >> 8, pr = (t >> 2) & 63, q = t & 3;
   float* pbase = const_cast<float*>(part);
   float2 ml = make_float2(0.f, 0.f);
-  if (t < 2 * nch) ml = ld_coh2(part_ptr(pbase, h, t % nch, t / nch));
+  const int mj = t >= nch ? 1 : 0, mc = t - mj * nch;   // (query head, chunk) of t < 2 nch
+  if (t < 2 * nch) ml = ld_coh2(part_ptr(pbase, h, mc, mj));
   float2 o2[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int c = q + 4 * i;
     o2[i] = c < nch ? ld_coh2(part_ptr(pbase, h, c, j) + 4 + 2 * pr) : make_float2(0.f, 0.f);
   }
-  if (t < 2 * nch) reinterpret_cast<float2*>(mw)[(t / nch) * 64 + t % nch] = ml;
+  if (t < 2 * nch) reinterpret_cast<float2*>(mw)[mj * 64 + mc] = ml;
   __syncthreads();
   if (t < 2 * 64) {
     // wave 0 and wave 1 (lanes = chunks) compute the weights of query head t / 64
@@ -535,8 +564,12 @@ MQ_DEV void attn_merge_head(const float* part, int h, int nch, float* att, float
     float o = 0.f;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) o += msum[(qq * 2 + jj) * 128 + d];
-    st_coh(att + (2 * h + jj) * MQ_D + d, o);
+    out(jj, d, o);
   }
+}
+MQ_DEV void attn_merge_head(const float* part, int h, int nch, float* att, float* lds) {
+  attn_merge(part, h, nch, lds,
+             [&](int jj, int d, float o) { st_coh(att + (2 * h + jj) * MQ_D + d, o); });
 }
 
 // Attention item of workgroup wg (items are (kv head h, chunk c), wg = c * NKV + h, so that
@@ -554,36 +587,6 @@ MQ_DEV AttnItem attn_item(int wg, int nch, int cache_len) {
   it.p0 = it.c * clen;
   it.p1 = min(cache_len, it.p0 + clen);
   return it;
-}
-
-// P2 for an active item (inputs already in LDS, first K/V block in `kv`).  With one chunk per
-// head the item normalises and writes att directly; otherwise it publishes its partial and the
-// last chunk of the head to arrive (per-head counter, monotone within the step) merges them.
-MQ_DEV void attn_run(const MqDecodeParams& p, int layer, const MqLayerW& w, int pos, int nch,
-                     const AttnItem& it, KvBlock& kv, float* lds) {
-  const int cache_len = pos + 1;
-  float* s_att = p.s->att;
-  attn_prologue(p, layer, w, it.h, pos, it.p1 == cache_len, lds);
-  attn_stat_init(lds);
-  __syncthreads();
-  attn_core(p, layer, it.h, it.p0, it.p1, pos, kv, lds);
-  if (nch == 1) {
-    if (tid() < 256)
-      st_coh(s_att + 2 * it.h * MQ_D + tid(),
-             lds[ALDS_ORED + tid()] / lds[ALDS_STAT + 2 + (tid() >> 7)]);
-    return;
-  }
-  attn_write_partial(p.s->part, it.h, it.c, lds);
-  wait_all_memory();
-  __syncthreads();
-  __shared__ int s_last;
-  if (tid() == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(&p.st->sync.attn[it.h].v, 1u, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (old == (uint32_t)((layer + 1) * nch - 1));
-  }
-  __syncthreads();
-  if (s_last) attn_merge_head(p.s->part, it.h, nch, s_att, lds);
 }
 
 // ---------------------------------------------------------------------------- P3: O proj
@@ -742,6 +745,211 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
   }
 }
 
+// ------------------------------------------------------------------- head-group decode
+// The persistent kernel assigns workgroup wg to kv-head group h = wg % 8 with index j = wg / 8
+// (NG = G / 8 workgroups per group).  Workgroups are dispatched round-robin over the 8 XCDs, so
+// a group shares one XCD and its L2; every exchange still uses device-scope (sc1) operations, so
+// correctness does not depend on that placement, only the cost of the group-local steps does.
+// Per layer:
+//   1. q|k|v: group h computes the 512 rows of its kv head (q heads 2h, 2h+1, k and v of h).
+//   2. group barrier; attention split over the group's workgroups by position chunks, partials
+//      (m, l, o) published per chunk.
+//   3. group barrier; every workgroup of the group merges the partials (att of its two query
+//      heads) and computes its rows of the O projection restricted to the head's 256 columns.
+//   4. grid barrier; a = x + sum_h opart_h, RMSNorm, gate|up rows.
+//   5. grid barrier; down rows + a -> bf16 layer output.   6. grid barrier -> next layer.
+// That is 3 grid-wide and 2 group-local barriers per layer.
+
+// Local row i of group h's 512 q|k|v rows -> row of the fused q|k|v projection.
+MQ_DEV int grp_row(int h, int i) {
+  if (i < 2 * MQ_D) return 2 * h * MQ_D + i;
+  if (i < 3 * MQ_D) return MQ_QDIM + h * MQ_D + (i - 2 * MQ_D);
+  return MQ_QDIM + MQ_KVDIM + h * MQ_D + (i - 3 * MQ_D);
+}
+MQ_DEV void gqkv_load(QkvSet& ws, const MqLayerW& w, int h, int j, int NG) {
+  int r0, nr;
+  row_range(4 * MQ_D, j, NG, r0, nr);
+  ws.load([&](int i) { return qkv_row(w, grp_row(h, r0 + i)); }, nr);
+}
+MQ_DEV void gqkv_run(const QkvSet& ws, const MqLayerW& w, int h, int j, int NG, float* lds) {
+  norm_1024(lds + LDS_IN, w.in_ln, lds + LDS_XN, lds + LDS_RED);
+  __syncthreads();
+  int r0, nr;
+  row_range(4 * MQ_D, j, NG, r0, nr);
+  ws.compute([&](int i) { return qkv_row(w, grp_row(h, r0 + i)); }, nr, lds + LDS_XN,
+             [&](int it, float v) { lds[LDS_PR + it] = v; });
+}
+MQ_DEV void gqkv_publish(float* qkv, int h, int j, int NG, const float* lds) {
+  int r0, nr;
+  row_range(4 * MQ_D, j, NG, r0, nr);
+  for (int t = lane_id(); t < nr; t += 64) st_coh(qkv + grp_row(h, r0 + t), lds[LDS_PR + t]);
+}
+
+// Position chunks of a group: as many chunks of at least one register slot (28 positions) as
+// the group has workgroups; chunk j = [p0, p1).  All chunks c < nch are non-empty.
+struct GAttn {
+  int nch, p0, p1;
+  bool active, has_pos;
+};
+MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos) {
+  GAttn g;
+  const int want = (cache_len + MQ_ATT_SLOT - 1) / MQ_ATT_SLOT;
+  const int n0 = min(min(NG, MQ_MAX_CHUNKS), want);
+  const int clen = (cache_len + n0 - 1) / n0;
+  g.nch = (cache_len + clen - 1) / clen;
+  g.p0 = j * clen;
+  g.p1 = min(cache_len, g.p0 + clen);
+  g.active = j < g.nch;
+  g.has_pos = g.active && pos >= g.p0 && pos < g.p1;
+  return g;
+}
+// Sync wave, after attn_core: this chunk's partial (m, l, o) of both query heads, and the new
+// position's K/V cache row from the chunk that holds it.
+MQ_DEV void gattn_publish(const MqDecodeParams& p, int layer, int pos, int h, int j,
+                          const GAttn& g, const float* lds) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = lane + 64 * i, jj = t >> 7, d = t & 127;
+    st_coh(part_ptr(p.s->part, h, j, jj) + 4 + d, lds[ALDS_ORED + t]);
+  }
+  if (lane < 2) {
+    st_coh(part_ptr(p.s->part, h, j, lane), lds[ALDS_STAT + lane]);
+    st_coh(part_ptr(p.s->part, h, j, lane) + 1, lds[ALDS_STAT + 2 + lane]);
+  }
+  if (g.has_pos) attn_cache_row(p, layer, h, pos, lds);
+}
+// All threads: merged attention output of query heads 2h, 2h+1 into LDS_ATTH.
+MQ_DEV void group_merge(const float* part, int h, int nch, float* lds) {
+  attn_merge(part, h, nch, lds, [&](int jj, int d, float o) { lds[LDS_ATTH + jj * MQ_D + d] = o; });
+  __syncthreads();
+}
+
+// GEMV over rows of 256 elements (the O projection restricted to one kv head's two query
+// heads): one wave instruction covers a pair of rows, lanes 0-31 the first and 32-63 the second.
+template <int PF>
+struct PairSet {
+  uint4 w[PF];
+  template <class RowPtr>
+  MQ_DEV void load(RowPtr rowptr, int nr) {
+    const int lane = lane_id(), wave = wave_id();
+    if (wave >= MQ_CWAVES) return;
+    const int np = (nr + 1) / 2;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int it = wave + i * MQ_CWAVES, row = 2 * it + (lane >> 5);
+      w[i] = (it < np && row < nr) ? ld_nt16(rowptr(row) + (lane & 31) * 8)
+                                   : make_uint4(0, 0, 0, 0);
+    }
+  }
+  template <class RowPtr, class Out>
+  MQ_DEV void compute(RowPtr rowptr, int nr, const float* __restrict__ x, Out out) const {
+    const int lane = lane_id(), wave = wave_id();
+    if (wave >= MQ_CWAVES) return;
+    const int np = (nr + 1) / 2;
+    const float* xs = x + (lane & 31) * 8;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int it = wave + i * MQ_CWAVES, row = 2 * it + (lane >> 5);
+      if (it < np) {
+        const float acc = sum_xor16(row16_sum(dot8_lds(w[i], xs, 0.f)));
+        if ((lane & 31) == 0 && row < nr) out(row, acc);
+      }
+    }
+    for (int it = wave + PF * MQ_CWAVES; it < np; it += MQ_CWAVES) {
+      const int row = 2 * it + (lane >> 5);
+      const uint4 v = row < nr ? ld_nt16(rowptr(row) + (lane & 31) * 8) : make_uint4(0, 0, 0, 0);
+      const float acc = sum_xor16(row16_sum(dot8_lds(v, xs, 0.f)));
+      if ((lane & 31) == 0 && row < nr) out(row, acc);
+    }
+  }
+};
+typedef PairSet<3> OPairSet;   // 32 rows (16 pairs) per workgroup at 256 workgroups
+
+MQ_DEV const bf16_t* opart_row(const MqLayerW& w, int h, int r) {
+  return w.wo + (size_t)r * MQ_QDIM + 2 * h * MQ_D;
+}
+MQ_DEV void opart_load(OPairSet& ws, const MqLayerW& w, int h, int j, int NG) {
+  int r0, nr;
+  row_range(MQ_H, j, NG, r0, nr);
+  ws.load([&](int i) { return opart_row(w, h, r0 + i); }, nr);
+}
+// Input: att of the group's query heads in LDS_ATTH; dot products -> LDS_PR.
+MQ_DEV void opart_run(const OPairSet& ws, const MqLayerW& w, int h, int j, int NG, float* lds) {
+  int r0, nr;
+  row_range(MQ_H, j, NG, r0, nr);
+  ws.compute([&](int i) { return opart_row(w, h, r0 + i); }, nr, lds + LDS_ATTH,
+             [&](int i, float v) { lds[LDS_PR + i] = v; });
+}
+MQ_DEV void opart_publish(float* opart, int h, int j, int NG, const float* lds) {
+  int r0, nr;
+  row_range(MQ_H, j, NG, r0, nr);
+  for (int t = lane_id(); t < nr; t += 64) st_coh(opart + h * MQ_H + r0 + t, lds[LDS_PR + t]);
+}
+// a = x + sum_h opart_h, summed in head order (the single-row form for the multi-kernel mode).
+MQ_DEV float a_elem(float x, const float* opart, int r) {
+  float a = x;
+#pragma unroll
+  for (int h = 0; h < MQ_NKV; ++h) a += ld_coh(opart + h * MQ_H + r);
+  return a;
+}
+// Sync wave: a for all 1024 rows from the layer input in LDS_HID -> LDS_IN (gate|up input) and
+// LDS_A (residual of the down rows).  Loads of half the rows are issued before any is summed.
+MQ_DEV void gu_input(const float* opart, float* lds) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    float2 o[4][MQ_NKV];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int h = 0; h < MQ_NKV; ++h)
+        o[i][h] = ld_coh2(opart + h * MQ_H + 2 * (lane + 64 * (4 * b + i)));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = lane + 64 * (4 * b + i);
+      float2 a = reinterpret_cast<const float2*>(lds + LDS_HID)[q];
+#pragma unroll
+      for (int h = 0; h < MQ_NKV; ++h) {
+        a.x += o[i][h].x;
+        a.y += o[i][h].y;
+      }
+      reinterpret_cast<float2*>(lds + LDS_IN)[q] = a;
+      reinterpret_cast<float2*>(lds + LDS_A)[q] = a;
+    }
+  }
+}
+// Sync wave: the layer input into LDS_IN and LDS_HID (coherent fp32, or the bf16 embedding row).
+MQ_DEV void input_hidden_coh(float* lds, const float* src) {
+  const int lane = lane_id();
+  float2 v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = ld_coh2(src + 2 * (lane + 64 * i));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    reinterpret_cast<float2*>(lds + LDS_IN)[lane + 64 * i] = v[i];
+    reinterpret_cast<float2*>(lds + LDS_HID)[lane + 64 * i] = v[i];
+  }
+}
+MQ_DEV void input_hidden_bf16(float* lds, const bf16_t* src) {
+  wave_copy_bf16_1024(lds + LDS_IN, src);
+  wave_copy_bf16_1024(lds + LDS_HID, src);
+}
+
+// Phase boundary of the head-group kernel: like phase_sync, with the barrier passed in.
+template <class Epi, class Bar, class Input>
+MQ_DEV void phase_step(Epi epilogue, Bar barrier, Input input) {
+  __syncthreads();
+  if (wave_id() == MQ_SYNC_WAVE) {
+    epilogue();
+    wait_all_memory();
+    barrier();
+    input();
+    wait_all_memory();
+  }
+  __syncthreads();
+}
+
 // ------------------------------------------------------------------------------- kernels
 // Reads and validates the step's position and input token.  The result is identical in every
 // workgroup, so an invalid step makes all of them return before the first barrier.
@@ -766,72 +974,112 @@ MQ_DEV void stamp(const MqDecodeParams& p, int wg, int l, int k) {
     p.stamps[((size_t)wg * p.num_layers + l) * MQ_NSTAMP + k] = __builtin_amdgcn_s_memrealtime();
 }
 
+// Layer `l` of the weight-pointer table copied into LDS, moved to scalar registers: the pointers
+// are uniform, and reading them from LDS keeps them off the vector memory queue, where the
+// weight prefetches of the previous phase would delay them.
+MQ_DEV uintptr_t uniform_u64(uintptr_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+MQ_DEV MqLayerW lds_layer(const MqLayerW* table, int l) {
+  const MqLayerW& t = table[l];
+  MqLayerW w;
+#define MQ_U(f) w.f = reinterpret_cast<const bf16_t*>(uniform_u64(reinterpret_cast<uintptr_t>(t.f)))
+  MQ_U(in_ln); MQ_U(wq); MQ_U(wk); MQ_U(wv); MQ_U(q_norm); MQ_U(k_norm);
+  MQ_U(wo); MQ_U(post_ln); MQ_U(wg); MQ_U(wu); MQ_U(wd);
+#undef MQ_U
+  return w;
+}
+static_assert(sizeof(MqLayerW) == 11 * sizeof(void*), "MqLayerW holds exactly the 11 pointers");
+
 __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDecodeParams p) {
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
+  __shared__ MqLayerW s_layers[MQ_MAX_LAYERS];
   const int G = gridDim.x, wg = blockIdx.x;
   int pos, tok;
   if (!step_inputs(p, pos, tok)) return;
-  const int nch = mq_attn_nchunks(pos + 1, G);
-  const AttnItem item = attn_item(wg, nch, pos + 1);
+  {
+    const int nw = p.num_layers * (int)(sizeof(MqLayerW) / 4);
+    for (int i = tid(); i < nw; i += MQ_THREADS)
+      reinterpret_cast<uint32_t*>(s_layers)[i] = reinterpret_cast<const uint32_t*>(p.layers)[i];
+    __syncthreads();
+  }
+  const int h = wg % MQ_GROUPS, j = wg / MQ_GROUPS, NG = G / MQ_GROUPS;
+  const GAttn ga = gattn_plan(j, NG, pos + 1, pos);
   MqSync* sy = &p.st->sync;
   MqScratch* s = p.s;
   const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
+  const bf16_t* cs = p.cos + (size_t)pos * MQ_D;
+  const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
   int r0h, nrh;
   row_range(MQ_H, wg, G, r0h, nrh);
-  // residual of this workgroup's hidden rows, held by sync-wave lane t for row r0h + t
-  float res = lane_id() < nrh ? bf16_to_f32(xe[r0h + lane_id()]) : 0.f;
   uint32_t nbar = 0;
   QkvSet wq;
-  OSet wo;
+  OPairSet wo;
   GateUpSet wgu;
   DownSet wd;
   KvBlock kv;
-  if (p.num_layers > 0) qkv_load(wq, p.layers[0], wg, G);
-  phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_bf16_1024(lds + LDS_IN, xe); });
+  if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG);
+  phase_step(MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
   for (int l = 0; l < p.num_layers; ++l) {
-    const MqLayerW w = p.layers[l];
+    const MqLayerW w = lds_layer(s_layers, l);
     stamp(p, wg, l, 0);
-    qkv_run(wq, w, wg, G, lds);
+    // this layer's K/V chunk: issued before the q|k|v dot products so that it arrives during
+    // them and the group barrier (the group barrier alone is shorter than an HBM round trip)
+    if (ga.active)
+      kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
+                    min(ga.p1, ga.p0 + MQ_ATT_BLOCK));
+    gqkv_run(wq, w, h, j, NG, lds);
     stamp(p, wg, l, 1);
-    if (item.active)
-      kv_block_load(kv, kv_base(p.kc, p, l, item.h), kv_base(p.vc, p, l, item.h), item.p0,
-                    min(item.p1, item.p0 + MQ_ATT_BLOCK));
-    phase_sync(sy, (++nbar) * (uint32_t)G, true, [&] { qkv_publish(s->qkv, wg, G, lds); },
-               [&] { if (item.active) attn_input(s->qkv, item.h, lds); });
+    // gate|up weights two phases ahead: the attention phase leaves the memory queue idle
+    gu_load(wgu, w, wg, G);
+    phase_step([&] { gqkv_publish(s->qkv, h, j, NG, lds); },
+               [&] { group_barrier_wave(sy, h, (uint32_t)((2 * l + 1) * NG)); },
+               [&] { if (ga.active) attn_input(s->qkv, w.q_norm, w.k_norm, cs, sn, h, lds); });
     stamp(p, wg, l, 2);
-    if (item.active) {
-      attn_run(p, l, w, pos, nch, item, kv, lds);
-      wait_all_memory();
+    if (ga.active) {
+      attn_prologue(lds);
+      __syncthreads();
+      attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds);
     }
     stamp(p, wg, l, 3);
-    o_load(wo, w, wg, G);
-    phase_sync(sy, (++nbar) * (uint32_t)G, true, MQ_NOTHING,
-               [&] { wave_copy_coh<MQ_QDIM>(lds + LDS_IN, s->att); });
+    opart_load(wo, w, h, j, NG);
+    phase_step([&] { if (ga.active) gattn_publish(p, l, pos, h, j, ga, lds); },
+               [&] { group_barrier_wave(sy, h, (uint32_t)((2 * l + 2) * NG)); }, MQ_NOTHING);
     stamp(p, wg, l, 4);
-    o_run(wo, w, wg, G, lds);
+    group_merge(s->part, h, ga.nch, lds);
+    opart_run(wo, w, h, j, NG, lds);
     stamp(p, wg, l, 5);
-    gu_load(wgu, w, wg, G);
-    phase_sync(sy, (++nbar) * (uint32_t)G, true, [&] { o_publish(s->a, wg, G, lds, res); },
-               [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, s->a); });
+    phase_step([&] { opart_publish(&s->opart[0][0], h, j, NG, lds); },
+               [&] { grid_barrier_wave(sy, (++nbar) * (uint32_t)G); },
+               [&] { gu_input(&s->opart[0][0], lds); });
     stamp(p, wg, l, 6);
     gu_run(wgu, w, wg, G, lds);
     stamp(p, wg, l, 7);
     down_load(wd, w, wg, G);
-    phase_sync(sy, (++nbar) * (uint32_t)G, true, [&] { gu_publish(s->mlp, wg, G, lds); },
+    phase_step([&] { gu_publish(s->mlp, wg, G, lds); },
+               [&] { grid_barrier_wave(sy, (++nbar) * (uint32_t)G); },
                [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, s->mlp); });
     stamp(p, wg, l, 8);
     down_run(wd, w, wg, G, lds);
     stamp(p, wg, l, 9);
-    if (l + 1 < p.num_layers) qkv_load(wq, p.layers[l + 1], wg, G);
-    phase_sync(sy, (++nbar) * (uint32_t)G, true,
-               [&] { down_publish(wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); }); },
-               [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, s->hidden); });
+    if (l + 1 < p.num_layers) gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG);
+    phase_step(
+        [&] {
+          float res = lane_id() < nrh ? lds[LDS_A + r0h + lane_id()] : 0.f;
+          down_publish(wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); });
+        },
+        [&] { grid_barrier_wave(sy, (++nbar) * (uint32_t)G); },
+        [&] { input_hidden_coh(lds, s->hidden); });
     stamp(p, wg, l, 10);
   }
   lm_head_run(p, wg, G, lds, p.tok_out, p.logits, pos, true);
 }
 
-// One kernel per phase (kernel boundaries replace the grid barriers; residuals are re-read).
+// One kernel per phase of the head-group step (kernel boundaries replace the barriers).  Every
+// value is computed by the same functions in the same order as in the persistent kernel, so
+// both modes produce bit-identical results.
 template <int PH>
 __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodeParams p, int l) {
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
@@ -840,10 +1088,13 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
   if (!step_inputs(p, pos, tok)) return;
   MqScratch* s = p.s;
   MqSync* sy = &p.st->sync;
+  const int h = wg % MQ_GROUPS, j = wg / MQ_GROUPS, NG = G / MQ_GROUPS;
   const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
-  int r0h, nrh;
-  row_range(MQ_H, wg, G, r0h, nrh);
-  const int t = lane_id();
+  // the layer input: the embedding row for layer 0, else the previous layer's output
+  auto load_x = [&](float* dst) {
+    if (l == 0) wave_copy_bf16_1024(dst, xe);
+    else wave_copy_coh<MQ_H>(dst, s->hidden);
+  };
   if constexpr (PH == 5) {
     phase_sync(sy, 0, false, MQ_NOTHING, [&] {
       if (p.num_layers == 0) wave_copy_bf16_1024(lds + LDS_IN, xe);
@@ -852,48 +1103,59 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
     lm_head_run(p, wg, G, lds, p.tok_out, p.logits, pos, true);
   } else {
     const MqLayerW w = p.layers[l];
-    const int nch = mq_attn_nchunks(pos + 1, G);
     if constexpr (PH == 0) {
       QkvSet ws;
-      qkv_load(ws, w, wg, G);
-      phase_sync(sy, 0, false, MQ_NOTHING, [&] {
-        if (l == 0) wave_copy_bf16_1024(lds + LDS_IN, xe);
-        else wave_copy_coh<MQ_H>(lds + LDS_IN, s->hidden);
-      });
-      qkv_run(ws, w, wg, G, lds);
-      phase_finish([&] { qkv_publish(s->qkv, wg, G, lds); });
+      gqkv_load(ws, w, h, j, NG);
+      phase_sync(sy, 0, false, MQ_NOTHING, [&] { load_x(lds + LDS_IN); });
+      gqkv_run(ws, w, h, j, NG, lds);
+      phase_finish([&] { gqkv_publish(s->qkv, h, j, NG, lds); });
     }
     if constexpr (PH == 1) {
-      const AttnItem item = attn_item(wg, nch, pos + 1);
-      if (item.active) {
+      const GAttn ga = gattn_plan(j, NG, pos + 1, pos);
+      if (ga.active) {
         KvBlock kv;
-        kv_block_load(kv, kv_base(p.kc, p, l, item.h), kv_base(p.vc, p, l, item.h), item.p0,
-                      min(item.p1, item.p0 + MQ_ATT_BLOCK));
-        phase_sync(sy, 0, false, MQ_NOTHING, [&] { attn_input(s->qkv, item.h, lds); });
-        attn_run(p, l, w, pos, nch, item, kv, lds);
+        kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
+                      min(ga.p1, ga.p0 + MQ_ATT_BLOCK));
+        phase_sync(sy, 0, false, MQ_NOTHING, [&] {
+          attn_input(s->qkv, w.q_norm, w.k_norm, p.cos + (size_t)pos * MQ_D,
+                     p.sin + (size_t)pos * MQ_D, h, lds);
+        });
+        attn_prologue(lds);
+        __syncthreads();
+        attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds);
+        phase_finish([&] { gattn_publish(p, l, pos, h, j, ga, lds); });
       }
     }
     if constexpr (PH == 2) {
-      OSet ws;
-      o_load(ws, w, wg, G);
-      float res = 0.f;
-      if (t < nrh) res = l == 0 ? bf16_to_f32(xe[r0h + t]) : ld_coh(s->hidden + r0h + t);
-      phase_sync(sy, 0, false, MQ_NOTHING,
-                 [&] { wave_copy_coh<MQ_QDIM>(lds + LDS_IN, s->att); });
-      o_run(ws, w, wg, G, lds);
-      phase_finish([&] { o_publish(s->a, wg, G, lds, res); });
+      const GAttn ga = gattn_plan(j, NG, pos + 1, pos);
+      OPairSet ws;
+      opart_load(ws, w, h, j, NG);
+      group_merge(s->part, h, ga.nch, lds);
+      opart_run(ws, w, h, j, NG, lds);
+      phase_finish([&] { opart_publish(&s->opart[0][0], h, j, NG, lds); });
     }
     if constexpr (PH == 3) {
       GateUpSet ws;
       gu_load(ws, w, wg, G);
-      phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, s->a); });
+      phase_sync(sy, 0, false, MQ_NOTHING, [&] {
+        load_x(lds + LDS_HID);
+        wait_all_memory();
+        gu_input(&s->opart[0][0], lds);
+      });
       gu_run(ws, w, wg, G, lds);
       phase_finish([&] { gu_publish(s->mlp, wg, G, lds); });
     }
     if constexpr (PH == 4) {
       DownSet ws;
       down_load(ws, w, wg, G);
-      float res = t < nrh ? ld_coh(s->a + r0h + t) : 0.f;
+      int r0h, nrh;
+      row_range(MQ_H, wg, G, r0h, nrh);
+      const int t = lane_id();
+      float res = 0.f;
+      if (wave_id() == MQ_SYNC_WAVE && t < nrh) {
+        const float x = l == 0 ? bf16_to_f32(xe[r0h + t]) : ld_coh(s->hidden + r0h + t);
+        res = a_elem(x, &s->opart[0][0], r0h + t);
+      }
       phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, s->mlp); });
       down_run(ws, w, wg, G, lds);
       phase_finish([&] {
@@ -916,12 +1178,17 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_qkv_kernel(MqDecodeParams p,
 }
 __global__ void __launch_bounds__(MQ_THREADS) mq_op_rope_kernel(MqDecodeParams p, int l, int pos,
                                                                  float* q_out) {
-  __shared__ __align__(16) float lds[1024];
+  __shared__ __align__(16) float lds[ALDS_WML];
   const int h = blockIdx.x;
-  phase_sync(&p.st->sync, 0, false, MQ_NOTHING, [&] { attn_input(p.s->qkv, h, lds); });
-  attn_prologue(p, l, p.layers[l], h, pos, true, lds);
+  const MqLayerW w = p.layers[l];
+  phase_sync(&p.st->sync, 0, false, MQ_NOTHING, [&] {
+    attn_input(p.s->qkv, w.q_norm, w.k_norm, p.cos + (size_t)pos * MQ_D,
+               p.sin + (size_t)pos * MQ_D, h, lds);
+  });
+  attn_prologue(lds);
   __syncthreads();
   if (tid() < 256) q_out[2 * h * MQ_D + tid()] = lds[ALDS_QS + tid()];
+  if (wave_id() == MQ_SYNC_WAVE) attn_cache_row(p, l, h, pos, lds);
 }
 // (b) attention of pre-rotated queries over cache rows [0, cache_len) -> partials, then merge.
 __global__ void __launch_bounds__(MQ_THREADS) mq_op_attn_kernel(MqDecodeParams p, int l,
@@ -934,7 +1201,6 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_attn_kernel(MqDecodeParams p
   kv_block_load(kv, kv_base(p.kc, p, l, it.h), kv_base(p.vc, p, l, it.h), it.p0,
                 min(it.p1, it.p0 + MQ_ATT_BLOCK));
   if (tid() < 256) lds[ALDS_QS + tid()] = q_hat[2 * it.h * MQ_D + tid()];
-  attn_stat_init(lds);
   __syncthreads();
   attn_core(p, l, it.h, it.p0, it.p1, -1, kv, lds);
   attn_write_partial(p.s->part, it.h, it.c, lds);
@@ -1044,7 +1310,8 @@ int mq_decode_grid(int mode, int* grid_out) {
   if (mode == MQ_MODE_PERSISTENT) {
     if (!g_coop_ok || g_persist_blocks_per_cu < 1) return -2;
   }
-  *grid_out = g_cu_count;  // one 512-thread workgroup per CU
+  // one 512-thread workgroup per CU, a whole number of kv-head groups (8)
+  *grid_out = g_cu_count / MQ_GROUPS * MQ_GROUPS;
   return 0;
 }
 
@@ -1054,7 +1321,7 @@ static int launch_status() {
 }
 
 int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t stream) {
-  if (grid < 64 || grid > 4096) return -3;
+  if (grid < 64 || grid > 4096 || grid % MQ_GROUPS != 0) return -3;
   if (mode == MQ_MODE_PERSISTENT) {
     MqDecodeParams pc = p;
     void* args[] = {&pc};

@@ -20,6 +20,10 @@
 #define MQ_SYNC_WAVE 7
 
 #define MQ_MAX_CHUNKS 64                // attention split-K chunks per kv head (upper bound)
+#define MQ_MAX_LAYERS 64                // decoder layers (the persistent kernel keeps their
+                                        // weight-pointer table in LDS)
 #define MQ_PART_STRIDE 132              // floats per attention partial: m, l, pad, pad, o[128]
 #define MQ_ATT_NK 8                     // positions per compute-wave row per attention block
 #define MQ_ATT_BLOCK (4 * MQ_CWAVES * MQ_ATT_NK)   // 224 positions scored per pass of a chunk
+#define MQ_ATT_SLOT (4 * MQ_CWAVES)     // 28 positions: one register slot of every compute wave
+#define MQ_GROUPS MQ_NKV                // persistent decode: workgroup wg serves kv head wg % 8

@@ -35,6 +35,7 @@ struct MqScratch {
   float hidden[MQ_H];          // residual stream at a layer boundary: bf16-rounded values (the
                                // reference keeps it in bf16, fused_decode_ldg_mlp.inl:200)
   float part[MQ_NKV * MQ_MAX_CHUNKS * MQ_GQA * MQ_PART_STRIDE];  // attention split-K partials
+  float opart[MQ_NKV][MQ_H];   // per-kv-head O-projection partials: W_o[:, head h cols] att_h
 };
 
 struct MqState {

@@ -56,6 +56,14 @@ MQ_DEV float dot8_lds(uint4 w, const float* x_lds, float acc) {
   float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   return dot8(w, xs, acc);
 }
+// Eight bf16-exact fp32 values (e.g. from LDS) packed back into 16 bytes of bf16.
+MQ_DEV uint4 pack8_bf16(const float* x) {
+  uint32_t u[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    u[i] = (__float_as_uint(x[2 * i]) >> 16) | (__float_as_uint(x[2 * i + 1]) & 0xffff0000u);
+  return make_uint4(u[0], u[1], u[2], u[3]);
+}
 MQ_DEV void unpack8(uint4 w, float* o) {
   o[0] = bf16_lo(w.x); o[1] = bf16_hi(w.x);
   o[2] = bf16_lo(w.y); o[3] = bf16_hi(w.y);
@@ -90,23 +98,35 @@ MQ_DEV float row16_max(float v) {
   v = fmaxf(v, dpp_f<MQ_DPP_ROW_MIRROR>(v));
   return v;
 }
-// Cross-row steps go through ds_bpermute (LDS crossbar, no LDS storage).
+// Arbitrary lane exchange through ds_bpermute (LDS crossbar, no LDS storage).
 MQ_DEV float xor_lane(float v, int mask) {
   int lane = __lane_id();
   return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
 }
+// Cross-row steps with the gfx950 row swaps (VALU, no LDS round trip).  With both operands x,
+// v_permlane16_swap returns (rows 0,0,2,2 of x ; rows 1,1,3,3 of x) and v_permlane32_swap returns
+// (lanes 0-31 twice ; lanes 32-63 twice), so the pair's sum (or max) is the value combined with
+// lane ^ 16 (^ 32), identical in both lanes of a pair.
+MQ_DEV float2 swap16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+MQ_DEV float2 swap32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+MQ_DEV float sum_xor16(float v) { const float2 p = swap16(v); return p.x + p.y; }
+MQ_DEV float sum_xor32(float v) { const float2 p = swap32(v); return p.x + p.y; }
+MQ_DEV float max_xor16(float v) { const float2 p = swap16(v); return fmaxf(p.x, p.y); }
+MQ_DEV float max_xor32(float v) { const float2 p = swap32(v); return fmaxf(p.x, p.y); }
 // Sum over all 64 lanes; every lane receives the total.
 MQ_DEV float wave_sum(float v) {
-  v = row16_sum(v);
-  v += xor_lane(v, 16);
-  v += xor_lane(v, 32);
-  return v;
+  return sum_xor32(sum_xor16(row16_sum(v)));
 }
 MQ_DEV float wave_max(float v) {
-  v = row16_max(v);
-  v = fmaxf(v, xor_lane(v, 16));
-  v = fmaxf(v, xor_lane(v, 32));
-  return v;
+  return max_xor32(max_xor16(row16_max(v)));
 }
 
 // Workgroup sum of one value per thread; `red` is MQ_WAVES floats of LDS.  All threads
@@ -182,7 +202,8 @@ struct alignas(128) MqLine64 {
 #define MQ_BAR_STRIPES 16
 struct MqSync {
   MqLine bar[MQ_BAR_STRIPES];  // striped grid-barrier arrival counters (reset at step end)
-  MqLine attn[MQ_NKV];         // per-kv-head split-K completion counters (reset at step end)
+  MqLine attn[MQ_NKV];         // per-kv-head group barrier / split-K completion counters
+                               // (reset at step end)
   MqLine done;                 // LM-head completion counter
   MqLine err;                  // nonzero after a barrier timed out or a bound was violated
   MqLine64 argmax;             // packed (value, index) key of the running vocabulary argmax
@@ -223,6 +244,30 @@ MQ_DEV void grid_barrier_wave(MqSync* s, uint32_t target) {
     const uint32_t e = __builtin_amdgcn_readlane(v, 63);
     const uint32_t total = __builtin_amdgcn_readfirstlane(row16_sum_u32(v));
     if (e != 0 || (int32_t)(total - target) >= 0) break;
+    if (++spins > MQ_SPIN_LIMIT) {
+      if (lane == 0)
+        __hip_atomic_store(&s->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+  }
+}
+
+// Barrier of one kv-head group (the NG workgroups of one XCD in the persistent kernel), executed
+// by the sync wave: arrival counter attn[h] is cumulative within a step like the grid stripes.
+MQ_DEV void group_barrier_wave(MqSync* s, int h, uint32_t target) {
+  const int lane = __lane_id();
+  if (lane == 0)
+    __hip_atomic_fetch_add(&s->attn[h].v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t spins = 0;
+  while (true) {
+    uint32_t v = 0;
+    if (lane == 0)
+      v = __hip_atomic_load(&s->attn[h].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else if (lane == 63)
+      v = __hip_atomic_load(&s->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t e = __builtin_amdgcn_readlane(v, 63);
+    const uint32_t c = __builtin_amdgcn_readlane(v, 0);
+    if (e != 0 || (int32_t)(c - target) >= 0) break;
     if (++spins > MQ_SPIN_LIMIT) {
       if (lane == 0)
         __hip_atomic_store(&s->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
