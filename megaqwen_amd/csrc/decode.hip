@@ -53,7 +53,9 @@ static_assert(MQ_SYNC_WAVE == MQ_CWAVES && MQ_CWAVES + 1 == MQ_WAVES, "one sync 
 #define LDS_HID 4608      // [1024] the layer input (residual of the attention block)
 #define LDS_A 5632        // [1024] a = layer input + attention block output (MLP residual)
 #define LDS_ATTH 0        // [256]  merged attention output of the group's two query heads
-#define MQ_LDS_FLOATS 6656
+#define LDS_AROW 6656     // [MQ_CWAVES * 4][256] attention: unnormalised p.V of each position row
+#define LDS_AL (LDS_AROW + MQ_CWAVES * 4 * 256)   // [MQ_CWAVES * 4][2] row sums of p
+#define MQ_LDS_FLOATS (LDS_AL + MQ_CWAVES * 4 * 2)
 
 // Balanced contiguous row range of workgroup `wg` out of `G` for an `n`-row matrix.
 MQ_DEV void row_range(int n, int wg, int G, int& r0, int& nr) {
@@ -182,6 +184,10 @@ MQ_DEV void phase_finish(Epi epilogue) {
   if (wave_id() == MQ_SYNC_WAVE) epilogue();
 }
 #define MQ_NOTHING [] {}
+
+// 2^x with the hardware v_exp_f32 (results below the normal range flush to zero, as the
+// reference's fast-math __expf does); used for softmax weights, whose arguments are <= 0.
+MQ_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------------------- RMSNorm
 // xn = x * rsqrt(mean(x^2) + eps) * w over the 1024 values in LDS `x`, two per thread.
@@ -427,8 +433,8 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
       mx1 = max_xor32(max_xor16(mx1));
       const float n0 = fmaxf(m0, mx0), n1 = fmaxf(m1, mx1);
       // rescale of what this wave accumulated so far (nothing yet while its max is -inf)
-      const float al0 = n0 == -INFINITY ? 1.f : exp2f(m0 - n0);
-      const float al1 = n1 == -INFINITY ? 1.f : exp2f(m1 - n1);
+      const float al0 = n0 == -INFINITY ? 1.f : exp2_fast(m0 - n0);
+      const float al1 = n1 == -INFINITY ? 1.f : exp2_fast(m1 - n1);
       l0 *= al0;
       l1 *= al1;
 #pragma unroll
@@ -440,8 +446,8 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
       for (int k = 0; k < MQ_ATT_NK; ++k) {
         if (k >= nk) break;
         const int pp = blk + k * 4 * MQ_CWAVES + wave * 4 + g;
-        const float w0 = pp < bend ? exp2f(wsc[k * 4 + g] - n0) : 0.f;
-        const float w1 = pp < bend ? exp2f(wsc[32 + k * 4 + g] - n1) : 0.f;
+        const float w0 = pp < bend ? exp2_fast(wsc[k * 4 + g] - n0) : 0.f;
+        const float w1 = pp < bend ? exp2_fast(wsc[32 + k * 4 + g] - n1) : 0.f;
         l0 += w0;
         l1 += w1;
         float vv[8];
@@ -455,30 +461,25 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
       m0 = n0;
       m1 = n1;
     }
-    // sum the wave's 4 position rows
+    // each position row leaves its p.V and sum of p in LDS; rows and waves are combined in the
+    // merge below (cheaper than reducing across rows in registers)
+    float* arow = lds + LDS_AROW + (wave * 4 + g) * 256;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      acc0[e] = sum_xor32(sum_xor16(acc0[e]));
-      acc1[e] = sum_xor32(sum_xor16(acc1[e]));
+      arow[sub * 8 + e] = acc0[e];
+      arow[MQ_D + sub * 8 + e] = acc1[e];
     }
-    l0 = sum_xor32(sum_xor16(l0));
-    l1 = sum_xor32(sum_xor16(l1));
-    if (g == 0) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        ored[wave * 256 + sub * 8 + e] = acc0[e];
-        ored[wave * 256 + MQ_D + sub * 8 + e] = acc1[e];
-      }
+    if (sub == 0) {
+      lds[LDS_AL + (wave * 4 + g) * 2 + 0] = l0;
+      lds[LDS_AL + (wave * 4 + g) * 2 + 1] = l1;
     }
     if (lane == 0) {
       wml[wave * 4 + 0] = m0;
       wml[wave * 4 + 1] = m1;
-      wml[wave * 4 + 2] = l0;
-      wml[wave * 4 + 3] = l1;
     }
   }
   __syncthreads();
-  // merge the compute waves (every item has at least one valid position, so M is finite)
+  // merge the compute waves' rows (every item has at least one valid position, so M is finite)
   if (tid() < 256) {
     const int j = tid() >> 7;
     float M = -INFINITY;
@@ -488,11 +489,15 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
 #pragma unroll
     for (int w8 = 0; w8 < MQ_CWAVES; ++w8) {
       const float mw = wml[w8 * 4 + j];
-      const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
-      o = fmaf(f, ored[w8 * 256 + tid()], o);
-      L = fmaf(f, wml[w8 * 4 + 2 + j], L);
+      const float f = mw == -INFINITY ? 0.f : exp2_fast(mw - M);
+      const float* ar = lds + LDS_AROW + w8 * 4 * 256 + tid();
+      const float* al = lds + LDS_AL + w8 * 4 * 2 + j;
+      const float ow = (ar[0] + ar[256]) + (ar[512] + ar[768]);
+      const float lw = (al[0] + al[2]) + (al[4] + al[6]);
+      o = fmaf(f, ow, o);
+      L = fmaf(f, lw, L);
     }
-    ored[tid()] = o;   // each thread rewrites only the slot it alone read last
+    ored[tid()] = o;
     if ((tid() & 127) == 0) {
       stat[j] = M;
       stat[2 + j] = L;
@@ -919,6 +924,25 @@ MQ_DEV void gu_input(const float* opart, float* lds) {
     }
   }
 }
+// All threads: a for all 1024 rows (thread t: rows 2t, 2t+1), same summation order as
+// gu_input and a_elem; ends with __syncthreads.
+MQ_DEV void gu_input_all(const float* opart, float* lds) {
+  const int t = tid();
+  if (t < MQ_H / 2) {
+    float2 o[MQ_NKV];
+#pragma unroll
+    for (int h = 0; h < MQ_NKV; ++h) o[h] = ld_coh2(opart + h * MQ_H + 2 * t);
+    float2 a = reinterpret_cast<const float2*>(lds + LDS_HID)[t];
+#pragma unroll
+    for (int h = 0; h < MQ_NKV; ++h) {
+      a.x += o[h].x;
+      a.y += o[h].y;
+    }
+    reinterpret_cast<float2*>(lds + LDS_IN)[t] = a;
+    reinterpret_cast<float2*>(lds + LDS_A)[t] = a;
+  }
+  __syncthreads();
+}
 // Sync wave: the layer input into LDS_IN and LDS_HID (coherent fp32, or the bf16 embedding row).
 MQ_DEV void input_hidden_coh(float* lds, const float* src) {
   const int lane = lane_id();
@@ -936,14 +960,24 @@ MQ_DEV void input_hidden_bf16(float* lds, const bf16_t* src) {
   wave_copy_bf16_1024(lds + LDS_HID, src);
 }
 
-// Phase boundary of the head-group kernel: like phase_sync, with the barrier passed in.
-template <class Epi, class Bar, class Input>
-MQ_DEV void phase_step(Epi epilogue, Bar barrier, Input input) {
+// Phase boundary of the head-group kernel.  Order of the workgroup's memory operations: the
+// sync wave's output stores (waited for), its barrier arrival, then the compute waves' weight
+// prefetch, then the sync wave's barrier polls and input loads.  A workgroup's memory queue is
+// first-in first-out in practice, so arriving before the prefetch is issued keeps the arrival
+// from waiting behind tens of KB of weight loads, and the prefetch drains while the barrier
+// completes.
+template <class Epi, class Arrive, class Prefetch, class Wait, class Input>
+MQ_DEV void phase_step(Epi epilogue, Arrive arrive, Prefetch prefetch, Wait wait, Input input) {
   __syncthreads();
   if (wave_id() == MQ_SYNC_WAVE) {
     epilogue();
     wait_all_memory();
-    barrier();
+    arrive();
+  }
+  __syncthreads();
+  if (wave_id() < MQ_CWAVES) prefetch();
+  if (wave_id() == MQ_SYNC_WAVE) {
+    wait();
     input();
     wait_all_memory();
   }
@@ -1021,7 +1055,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
   DownSet wd;
   KvBlock kv;
   if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG);
-  phase_step(MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
+  phase_step(MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
   for (int l = 0; l < p.num_layers; ++l) {
     const MqLayerW w = lds_layer(s_layers, l);
     stamp(p, wg, l, 0);
@@ -1032,10 +1066,13 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
                     min(ga.p1, ga.p0 + MQ_ATT_BLOCK));
     gqkv_run(wq, w, h, j, NG, lds);
     stamp(p, wg, l, 1);
-    // gate|up weights two phases ahead: the attention phase leaves the memory queue idle
-    gu_load(wgu, w, wg, G);
+    // the gate|up weights go out two phases ahead, during the attention phase, from workgroups
+    // without an attention chunk; the others issue them after their chunk (a deep queue stalls
+    // the issue of loads and would delay the attention merge and publish)
     phase_step([&] { gqkv_publish(s->qkv, h, j, NG, lds); },
-               [&] { group_barrier_wave(sy, h, (uint32_t)((2 * l + 1) * NG)); },
+               [&] { group_barrier_arrive(sy, h); },
+               [&] { if (!ga.active) gu_load(wgu, w, wg, G); },
+               [&] { group_barrier_wait(sy, h, (uint32_t)((2 * l + 1) * NG)); },
                [&] { if (ga.active) attn_input(s->qkv, w.q_norm, w.k_norm, cs, sn, h, lds); });
     stamp(p, wg, l, 2);
     if (ga.active) {
@@ -1044,33 +1081,40 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds);
     }
     stamp(p, wg, l, 3);
-    opart_load(wo, w, h, j, NG);
     phase_step([&] { if (ga.active) gattn_publish(p, l, pos, h, j, ga, lds); },
-               [&] { group_barrier_wave(sy, h, (uint32_t)((2 * l + 2) * NG)); }, MQ_NOTHING);
+               [&] { group_barrier_arrive(sy, h); },
+               [&] {
+                 opart_load(wo, w, h, j, NG);
+                 if (ga.active) gu_load(wgu, w, wg, G);
+               },
+               [&] { group_barrier_wait(sy, h, (uint32_t)((2 * l + 2) * NG)); }, MQ_NOTHING);
     stamp(p, wg, l, 4);
     group_merge(s->part, h, ga.nch, lds);
     opart_run(wo, w, h, j, NG, lds);
     stamp(p, wg, l, 5);
     phase_step([&] { opart_publish(&s->opart[0][0], h, j, NG, lds); },
-               [&] { grid_barrier_wave(sy, (++nbar) * (uint32_t)G); },
-               [&] { gu_input(&s->opart[0][0], lds); });
+               [&] { grid_barrier_arrive(sy); }, MQ_NOTHING,
+               [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); }, MQ_NOTHING);
+    gu_input_all(&s->opart[0][0], lds);
     stamp(p, wg, l, 6);
     gu_run(wgu, w, wg, G, lds);
     stamp(p, wg, l, 7);
-    down_load(wd, w, wg, G);
     phase_step([&] { gu_publish(s->mlp, wg, G, lds); },
-               [&] { grid_barrier_wave(sy, (++nbar) * (uint32_t)G); },
+               [&] { grid_barrier_arrive(sy); },
+               [&] { down_load(wd, w, wg, G); },
+               [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); },
                [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, s->mlp); });
     stamp(p, wg, l, 8);
     down_run(wd, w, wg, G, lds);
     stamp(p, wg, l, 9);
-    if (l + 1 < p.num_layers) gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG);
     phase_step(
         [&] {
           float res = lane_id() < nrh ? lds[LDS_A + r0h + lane_id()] : 0.f;
           down_publish(wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); });
         },
-        [&] { grid_barrier_wave(sy, (++nbar) * (uint32_t)G); },
+        [&] { grid_barrier_arrive(sy); },
+        [&] { if (l + 1 < p.num_layers) gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG); },
+        [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); },
         [&] { input_hidden_coh(lds, s->hidden); });
     stamp(p, wg, l, 10);
   }

@@ -229,11 +229,13 @@ MQ_DEV uint32_t row16_sum_u32(uint32_t v) {
 // prefetches outstanding, so its polls are not queued behind them (gfx9 returns a wave's loads
 // in order).  Precondition: the compute waves have waited for the stores other workgroups will
 // read before the __syncthreads that precedes this call.
-MQ_DEV void grid_barrier_wave(MqSync* s, uint32_t target) {
-  const int lane = __lane_id();
-  if (lane == 0)
+MQ_DEV void grid_barrier_arrive(MqSync* s) {
+  if (__lane_id() == 0)
     __hip_atomic_fetch_add(&s->bar[blockIdx.x % MQ_BAR_STRIPES].v, 1u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+}
+MQ_DEV void grid_barrier_wait(MqSync* s, uint32_t target) {
+  const int lane = __lane_id();
   uint32_t spins = 0;
   while (true) {
     uint32_t v = 0;
@@ -251,13 +253,19 @@ MQ_DEV void grid_barrier_wave(MqSync* s, uint32_t target) {
     }
   }
 }
+MQ_DEV void grid_barrier_wave(MqSync* s, uint32_t target) {
+  grid_barrier_arrive(s);
+  grid_barrier_wait(s, target);
+}
 
 // Barrier of one kv-head group (the NG workgroups of one XCD in the persistent kernel), executed
 // by the sync wave: arrival counter attn[h] is cumulative within a step like the grid stripes.
-MQ_DEV void group_barrier_wave(MqSync* s, int h, uint32_t target) {
-  const int lane = __lane_id();
-  if (lane == 0)
+MQ_DEV void group_barrier_arrive(MqSync* s, int h) {
+  if (__lane_id() == 0)
     __hip_atomic_fetch_add(&s->attn[h].v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+MQ_DEV void group_barrier_wait(MqSync* s, int h, uint32_t target) {
+  const int lane = __lane_id();
   uint32_t spins = 0;
   while (true) {
     uint32_t v = 0;
