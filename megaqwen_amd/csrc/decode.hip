@@ -336,13 +336,16 @@ MQ_DEV void attn_cache_row(const MqDecodeParams& p, int layer, int h, int pos, c
 struct KvBlock {
   uint4 k[MQ_ATT_NK], v[MQ_ATT_NK];
 };
-MQ_DEV void kv_block_load(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int blk, int bend) {
+MQ_DEV void kv_block_load(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int blk, int bend,
+                          bool small = false) {
   const int lane = lane_id(), wave = wave_id();
-  if (wave >= MQ_CWAVES) return;
+  // small chunks (<= 28 positions): wave 0 holds position blk + 4k + row in slot k
+  if (wave >= (small ? 1 : MQ_CWAVES)) return;
 #pragma unroll
   for (int k = 0; k < MQ_ATT_NK; ++k) {
-    const int pp = blk + k * 4 * MQ_CWAVES + wave * 4 + (lane >> 4);
-    if (pp < bend) {
+    const int pp = small ? blk + k * 4 + (lane >> 4)
+                         : blk + k * 4 * MQ_CWAVES + wave * 4 + (lane >> 4);
+    if (pp < bend && (!small || k < MQ_ATT_SLOT / 4)) {
       b.k[k] = ld16(Kb + (size_t)pp * MQ_D);
       b.v[k] = ld16(Vb + (size_t)pp * MQ_D);
     } else {
@@ -362,7 +365,7 @@ MQ_DEV const bf16_t* kv_base(const bf16_t* cache, const MqDecodeParams& p, int l
 // ALDS_STAT and the unnormalised o[2][128] in ALDS_ORED[0..255] (reference:
 // fused_decode_ldg_common.inl:417-602).
 MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1, int pos_new,
-                      KvBlock& b, float* lds) {
+                      KvBlock& b, float* lds, bool small = false) {
   const float* qs = lds + ALDS_QS;
   const float* kn = lds + ALDS_KN;
   const float* vn = lds + ALDS_VN;
@@ -371,7 +374,10 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
   float* ored = lds + ALDS_ORED;
   const int lane = lane_id(), wave = wave_id();
   const int g = lane >> 4, sub = lane & 15;
-  if (wave < MQ_CWAVES) {
+  // small chunks (<= 28 positions, one block): wave 0 alone takes every position, slot k holding
+  // position blk + 4k + row, and the merge below has a single wave to combine
+  const int nwaves = small ? 1 : MQ_CWAVES;
+  if (wave < nwaves) {
     const bf16_t* Kb = kv_base(p.kc, p, layer, h);
     const bf16_t* Vb = kv_base(p.vc, p, layer, h);
     float q0[8], q1[8];
@@ -396,7 +402,7 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
         const uint4 knp = pack8_bf16(kn + sub * 8), vnp = pack8_bf16(vn + sub * 8);
 #pragma unroll
         for (int k = 0; k < MQ_ATT_NK; ++k) {
-          if (blk + k * 4 * MQ_CWAVES + wave * 4 + g == pos_new) {
+          if ((small ? blk + k * 4 + g : blk + k * 4 * MQ_CWAVES + wave * 4 + g) == pos_new) {
             b.k[k] = knp;
             b.v[k] = vnp;
           }
@@ -406,12 +412,13 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
       float* wsc = lds + ALDS_WSC + wave * 64;
       float mx0 = -INFINITY, mx1 = -INFINITY;
       // position slots k of this wave holding at least one position below bend (wave-uniform)
-      const int nk = min(MQ_ATT_NK, max(0, (bend - blk - wave * 4 + 4 * MQ_CWAVES - 1) /
-                                               (4 * MQ_CWAVES)));
+      const int nk = small ? (bend - blk + 3) / 4
+                           : min(MQ_ATT_NK, max(0, (bend - blk - wave * 4 + 4 * MQ_CWAVES - 1) /
+                                                      (4 * MQ_CWAVES)));
 #pragma unroll
       for (int k = 0; k < MQ_ATT_NK; ++k) {
         if (k >= nk) break;
-        const int pp = blk + k * 4 * MQ_CWAVES + wave * 4 + g;
+        const int pp = small ? blk + k * 4 + g : blk + k * 4 * MQ_CWAVES + wave * 4 + g;
         float kv[8];
         unpack8(b.k[k], kv);
         float d0 = 0.f, d1 = 0.f;
@@ -445,7 +452,7 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
 #pragma unroll
       for (int k = 0; k < MQ_ATT_NK; ++k) {
         if (k >= nk) break;
-        const int pp = blk + k * 4 * MQ_CWAVES + wave * 4 + g;
+        const int pp = small ? blk + k * 4 + g : blk + k * 4 * MQ_CWAVES + wave * 4 + g;
         const float w0 = pp < bend ? exp2_fast(wsc[k * 4 + g] - n0) : 0.f;
         const float w1 = pp < bend ? exp2_fast(wsc[32 + k * 4 + g] - n1) : 0.f;
         l0 += w0;
@@ -484,10 +491,12 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
     const int j = tid() >> 7;
     float M = -INFINITY;
 #pragma unroll
-    for (int w8 = 0; w8 < MQ_CWAVES; ++w8) M = fmaxf(M, wml[w8 * 4 + j]);
+    for (int w8 = 0; w8 < MQ_CWAVES; ++w8)
+      if (w8 < nwaves) M = fmaxf(M, wml[w8 * 4 + j]);
     float o = 0.f, L = 0.f;
 #pragma unroll
     for (int w8 = 0; w8 < MQ_CWAVES; ++w8) {
+      if (w8 >= nwaves) break;
       const float mw = wml[w8 * 4 + j];
       const float f = mw == -INFINITY ? 0.f : exp2_fast(mw - M);
       const float* ar = lds + LDS_AROW + w8 * 4 * 256 + tid();
@@ -794,7 +803,7 @@ MQ_DEV void gqkv_publish(float* qkv, int h, int j, int NG, const float* lds) {
 // the group has workgroups; chunk j = [p0, p1).  All chunks c < nch are non-empty.
 struct GAttn {
   int nch, p0, p1;
-  bool active, has_pos;
+  bool active, has_pos, small;
 };
 MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos) {
   GAttn g;
@@ -806,6 +815,9 @@ MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos) {
   g.p1 = min(cache_len, g.p0 + clen);
   g.active = j < g.nch;
   g.has_pos = g.active && pos >= g.p0 && pos < g.p1;
+  // one wave has no other wave to hide its dependent reduction steps: it wins only for chunks of
+  // at most two position slots (measured 1.5 against 2.0 us at 4 positions, 3.5 against 2.2 at 28)
+  g.small = clen <= 8;
   return g;
 }
 // Sync wave, after attn_core: this chunk's partial (m, l, o) of both query heads, and the new
@@ -988,8 +1000,11 @@ MQ_DEV void phase_step(Epi epilogue, Arrive arrive, Prefetch prefetch, Wait wait
 // Reads and validates the step's position and input token.  The result is identical in every
 // workgroup, so an invalid step makes all of them return before the first barrier.
 MQ_DEV bool step_inputs(const MqDecodeParams& p, int& pos, int& tok) {
-  pos = (int)__hip_atomic_load(&p.st->pos.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  tok = *p.tok_in;
+  // uniform by construction; readfirstlane lets the compiler treat everything derived from them
+  // as scalar (uniform branches, no per-lane copies of alternative code paths)
+  pos = __builtin_amdgcn_readfirstlane(
+      (int)__hip_atomic_load(&p.st->pos.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  tok = __builtin_amdgcn_readfirstlane(*p.tok_in);
   if (pos < 0 || pos >= p.max_seq || tok < 0 || tok >= p.vocab) {
     if (blockIdx.x == 0 && tid() == 0)
       __hip_atomic_store(&p.st->sync.err.v, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1061,14 +1076,16 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     stamp(p, wg, l, 0);
     // this layer's K/V chunk: issued before the q|k|v dot products so that it arrives during
     // them and the group barrier (the group barrier alone is shorter than an HBM round trip)
-    if (ga.active)
+    if (ga.active) {
       kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
-                    min(ga.p1, ga.p0 + MQ_ATT_BLOCK));
+                    min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
+    }
     gqkv_run(wq, w, h, j, NG, lds);
     stamp(p, wg, l, 1);
     // the gate|up weights go out two phases ahead, during the attention phase, from workgroups
-    // without an attention chunk; the others issue them after their chunk (a deep queue stalls
-    // the issue of loads and would delay the attention merge and publish)
+    // without an attention chunk; the others issue them once they have arrived at the grid
+    // barrier after the O projection (a deep queue stalls the issue of loads and would delay
+    // their attention, the partial merge and the O projection, which are on the critical path)
     phase_step([&] { gqkv_publish(s->qkv, h, j, NG, lds); },
                [&] { group_barrier_arrive(sy, h); },
                [&] { if (!ga.active) gu_load(wgu, w, wg, G); },
@@ -1078,22 +1095,20 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     if (ga.active) {
       attn_prologue(lds);
       __syncthreads();
-      attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds);
+      attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds, ga.small);
     }
     stamp(p, wg, l, 3);
     phase_step([&] { if (ga.active) gattn_publish(p, l, pos, h, j, ga, lds); },
                [&] { group_barrier_arrive(sy, h); },
-               [&] {
-                 opart_load(wo, w, h, j, NG);
-                 if (ga.active) gu_load(wgu, w, wg, G);
-               },
+               [&] { opart_load(wo, w, h, j, NG); },
                [&] { group_barrier_wait(sy, h, (uint32_t)((2 * l + 2) * NG)); }, MQ_NOTHING);
     stamp(p, wg, l, 4);
     group_merge(s->part, h, ga.nch, lds);
     opart_run(wo, w, h, j, NG, lds);
     stamp(p, wg, l, 5);
     phase_step([&] { opart_publish(&s->opart[0][0], h, j, NG, lds); },
-               [&] { grid_barrier_arrive(sy); }, MQ_NOTHING,
+               [&] { grid_barrier_arrive(sy); },
+               [&] { if (ga.active) gu_load(wgu, w, wg, G); },
                [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); }, MQ_NOTHING);
     gu_input_all(&s->opart[0][0], lds);
     stamp(p, wg, l, 6);
@@ -1159,14 +1174,14 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       if (ga.active) {
         KvBlock kv;
         kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
-                      min(ga.p1, ga.p0 + MQ_ATT_BLOCK));
+                      min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
         phase_sync(sy, 0, false, MQ_NOTHING, [&] {
           attn_input(s->qkv, w.q_norm, w.k_norm, p.cos + (size_t)pos * MQ_D,
                      p.sin + (size_t)pos * MQ_D, h, lds);
         });
         attn_prologue(lds);
         __syncthreads();
-        attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds);
+        attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds, ga.small);
         phase_finish([&] { gattn_publish(p, l, pos, h, j, ga, lds); });
       }
     }

@@ -79,6 +79,40 @@ def test_decode_long_context_chunks(small):
     dec.check()
 
 
+@pytest.mark.parametrize("ctx", [2000, 7300])
+def test_decode_long_chunks_after_prefill(ctx):
+    """Contexts where the per-group attention chunks exceed one register slot (28 positions:
+    cache_len > 896, the seven-wave path) and one 224-position block (cache_len > 7168, several
+    blocks per chunk).  The prompt is prefilled on the GPU; the oracle takes over the GPU's KV
+    cache, so the decode steps are compared on identical caches (teacher-forced, 2e-2), in both
+    decode modes."""
+    dec, orc, sp, _ = build_pair(2, 151936, ctx + 16, seed=6, norm_jitter=0.1, max_prefill=ctx)
+    toks = make_tokens(ctx, sp["vocab_size"], seed=ctx)
+    feed = make_tokens(6, sp["vocab_size"], seed=ctx + 1).tolist()
+    results = {}
+    for mode in ("persistent", "multi_kernel"):
+        dec.set_mode(mode)
+        dec.reset()
+        dec.prefill_step(toks)
+        orc.k_cache.copy_(dec.k_cache.float().cpu())
+        orc.v_cache.copy_(dec.v_cache.float().cpu())
+        orc.position = ctx
+        out = []
+        for i, t in enumerate(feed):
+            tok, lg = dec.decode_step_with_logits(t)
+            otok, olg = orc.decode_step(t)
+            err = float((lg.cpu() - olg).abs().max())
+            print(f"ctx {ctx} {mode} step {i}: logit error {err:.3e}")
+            assert err <= TOL, (mode, i, err)
+            if top2_margin(olg) > 2 * err + 1e-6:
+                assert tok == otok
+            out.append((tok, lg.cpu()))
+        results[mode] = out
+        dec.check()
+    for (ta, la), (tb, lb) in zip(results["persistent"], results["multi_kernel"]):
+        assert ta == tb and torch.equal(la, lb)
+
+
 def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
     e = torch.floor(torch.log2(x.abs().clamp_min(1e-30)))
     return torch.pow(2.0, e - 7)
