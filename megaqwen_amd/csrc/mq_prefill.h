@@ -10,6 +10,8 @@ struct MqPrefillBuffers {
   bf16_t* qkv;   // [n, 4096] q | k | v projections (q/k rotated in place)
   bf16_t* att;   // [n, 2048] attention output
   bf16_t* m;     // [n, 3072] silu(gate) * up
+  bf16_t* vt;    // [8 * 128, ldvt] V transposed (dims x positions) for the causal attention
+  int ldvt;      // max_n rounded up to 32
 };
 
 size_t mq_prefill_workspace_bytes(int max_n);

@@ -14,9 +14,10 @@
 // then the last row's final norm (bf16) and the LM-head argmax (fused_prefill_kernels.inl:655-824).
 //
 // GEMMs are C[M,N] = A[M,K] B[N,K]^T ("NT": activations and weights both K-contiguous) on
-// v_mfma_f32_32x32x16_bf16 with fp32 accumulation: 64x64 workgroup tiles, 4 waves of 32x32,
-// K staged through double-buffered LDS in steps of 32.  Consecutive workgroups walk N first, so
-// with N/64 a multiple of 8 all M tiles of one weight tile land on one XCD and share its L2.
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulation: 64x64 or 32x64 workgroup tiles, K staged
+// through double-buffered LDS in steps of 64, fed by a 4-step register ring of global loads.
+// Consecutive workgroups walk N first, so with N/64 a multiple of 8 all M tiles of one weight
+// tile land on one XCD and share its L2.
 #include "mq_prefill.h"
 
 #include <math.h>
@@ -26,6 +27,9 @@ typedef float mq_f32x16 __attribute__((ext_vector_type(16)));
 
 MQ_DEV mq_bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(mq_bf16x8, v); }
 MQ_DEV float silu_f(float x) { return x / (1.0f + expf(-x)); }
+MQ_DEV uint32_t pack_bf16x2(float a, float b) {
+  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+}
 
 // ------------------------------------------------------------------------- row kernels
 __global__ void __launch_bounds__(128) pf_embed_kernel(const bf16_t* __restrict__ embed,
@@ -112,44 +116,77 @@ struct GemmArgs {
   int ldc;
   const bf16_t* R;   // EPI_RESID: residual [M, N] (may alias C)
   int ldr;
+  bf16_t* Vt;        // EPI_STORE: columns [n1, N) also stored transposed, Vt[(col - n1) * ldvt + row]
+  int ldvt;
   int M, N, K;
 };
 
-#define GEMM_BM 64
 #define GEMM_BN 64
-#define GEMM_BK 32
-#define GEMM_LDS_STRIDE 40   // bf16 per LDS row: 32 + 8 padding
+#define GEMM_BK 64
+#define GEMM_LDS_STRIDE 72   // bf16 per LDS row: 64 + 8 padding (16-byte chunk c of row r at 9r + c)
+#define GEMM_STAGES 4        // K steps whose global loads are in flight in registers
 
-template <int EPI>
+// One BM x 64 tile of C per workgroup of 4 waves, K in steps of 64.  The global loads of step
+// k + GEMM_STAGES are issued while step k is multiplied: a ring of GEMM_STAGES register slots
+// feeds a double-buffered LDS tile, so about 4 x 16 KB per workgroup are in flight.
+//   BM = 64: waves form a 2 x 2 grid of 32 x 32 blocks.
+//   BM = 32: waves 0/1 and 2/3 compute the same two 32 x 32 blocks over the first and the
+//            second half of every K step; the halves are added in LDS before the epilogue
+//            (this doubles the workgroups of the N = 1024 GEMMs at M = 512).
+template <int EPI, int BM>
 __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
-  constexpr int NB = EPI == EPI_SWIGLU ? 2 : 1;
-  __shared__ __align__(16) bf16_t As[2][GEMM_BM * GEMM_LDS_STRIDE];
+  constexpr int NB = EPI == EPI_SWIGLU ? 2 : 1;   // weight tiles per step (gate and up)
+  constexpr int KG = BM == 32 ? 2 : 1;            // wave groups splitting each K step
+  constexpr int NA = BM / 32;                     // 16-byte A loads per thread per step
+  constexpr int NL = GEMM_BN / 32;                // 16-byte loads per weight tile per thread
+  constexpr int S = GEMM_STAGES;
+  static_assert(BM == 32 || BM == 64, "tile rows");
+  __shared__ __align__(16) bf16_t As[2][BM * GEMM_LDS_STRIDE];
   __shared__ __align__(16) bf16_t Bs[2][NB][GEMM_BN * GEMM_LDS_STRIDE];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int n_base = blockIdx.x * GEMM_BN, m_base = blockIdx.y * GEMM_BM;
+  const int wn = wave & 1;
+  const int wm = KG == 1 ? (wave >> 1) : 0;
+  const int wk = KG == 2 ? (wave >> 1) : 0;
+  const int n_base = blockIdx.x * GEMM_BN, m_base = blockIdx.y * BM;
   const bf16_t* B;
   if (n_base < g.n0) B = g.B0 + (size_t)n_base * g.K;
   else if (n_base < g.n1) B = g.B1 + (size_t)(n_base - g.n0) * g.K;
   else B = g.B2 + (size_t)(n_base - g.n1) * g.K;
-  const bf16_t* Bu = (EPI == EPI_SWIGLU) ? g.Bu + (size_t)n_base * g.K : nullptr;
+  const bf16_t* Bu = (EPI == EPI_SWIGLU) ? g.Bu + (size_t)n_base * g.K : B;
 
-  // global -> register staging: thread t moves 16 bytes of row t/4, k offset (t%4)*8
-  const int lr = t >> 2, lk = (t & 3) * 8;
-  const int am = m_base + lr;
-  const bool a_ok = am < g.M;
-  const bf16_t* a_src = g.A + (size_t)(a_ok ? am : g.M - 1) * g.lda + lk;
-  const bf16_t* b_src = B + (size_t)lr * g.K + lk;
-  const bf16_t* u_src = (EPI == EPI_SWIGLU) ? Bu + (size_t)lr * g.K + lk : nullptr;
-
-  uint4 ra = a_ok ? ld16(a_src) : make_uint4(0, 0, 0, 0);
-  uint4 rb[NB];
-  rb[0] = ld_nt16(b_src);
-  if (NB == 2) rb[NB - 1] = ld_nt16(u_src);
-  *reinterpret_cast<uint4*>(&As[0][lr * GEMM_LDS_STRIDE + lk]) = ra;
+  // global -> register staging: thread t moves 16-byte chunk t % 8 of rows t / 8 + 32 i.
+  // Rows past M read row M - 1 (their results are never stored).
+  const int sr = t >> 3, sk = (t & 7) * 8;
+  const bf16_t* a_src[NA];
 #pragma unroll
-  for (int b = 0; b < NB; ++b) *reinterpret_cast<uint4*>(&Bs[0][b][lr * GEMM_LDS_STRIDE + lk]) = rb[b];
-  __syncthreads();
+  for (int i = 0; i < NA; ++i) {
+    const int am = min(m_base + sr + 32 * i, g.M - 1);
+    a_src[i] = g.A + (size_t)am * g.lda + sk;
+  }
+  const bf16_t* b_src[NB];
+  b_src[0] = B + (size_t)sr * g.K + sk;
+  if (NB == 2) b_src[NB - 1] = Bu + (size_t)sr * g.K + sk;
+
+  uint4 ra[S][NA], rb[S][NB][NL];
+  auto load_step = [&](int k, uint4 (&a)[NA], uint4 (&b)[NB][NL]) {
+    const int k0 = k * GEMM_BK;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) a[i] = ld16(a_src[i] + k0);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int i = 0; i < NL; ++i) b[j][i] = ld16(b_src[j] + (size_t)(32 * i) * g.K + k0);
+  };
+  auto store_step = [&](int buf, const uint4 (&a)[NA], const uint4 (&b)[NB][NL]) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+      *reinterpret_cast<uint4*>(&As[buf][(sr + 32 * i) * GEMM_LDS_STRIDE + sk]) = a[i];
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int i = 0; i < NL; ++i)
+        *reinterpret_cast<uint4*>(&Bs[buf][j][(sr + 32 * i) * GEMM_LDS_STRIDE + sk]) = b[j][i];
+  };
 
   mq_f32x16 acc[NB];
 #pragma unroll
@@ -158,33 +195,57 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
     for (int j = 0; j < 16; ++j) acc[b][j] = 0.f;
 
   const int fr = lane & 31, fk = (lane >> 5) * 8;   // MFMA operand row and k offset of a lane
-  int cur = 0;
-  for (int k0 = 0; k0 < g.K; k0 += GEMM_BK) {
-    const bool more = k0 + GEMM_BK < g.K;
-    if (more) {
-      ra = a_ok ? ld16(a_src + k0 + GEMM_BK) : make_uint4(0, 0, 0, 0);
-      rb[0] = ld_nt16(b_src + k0 + GEMM_BK);
-      if (NB == 2) rb[NB - 1] = ld_nt16(u_src + k0 + GEMM_BK);
-    }
+  auto mma_step = [&](int buf) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int q = 0; q < 4 / KG; ++q) {
+      const int kofs = 16 * (q + wk * (4 / KG)) + fk;
       const mq_bf16x8 af = as_bf16x8(
-          *reinterpret_cast<const uint4*>(&As[cur][(wm * 32 + fr) * GEMM_LDS_STRIDE + 16 * s + fk]));
+          *reinterpret_cast<const uint4*>(&As[buf][(wm * 32 + fr) * GEMM_LDS_STRIDE + kofs]));
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const mq_bf16x8 bf = as_bf16x8(*reinterpret_cast<const uint4*>(
-            &Bs[cur][b][(wn * 32 + fr) * GEMM_LDS_STRIDE + 16 * s + fk]));
+            &Bs[buf][b][(wn * 32 + fr) * GEMM_LDS_STRIDE + kofs]));
         acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc[b], 0, 0, 0);
       }
     }
-    if (more) {
-      *reinterpret_cast<uint4*>(&As[cur ^ 1][lr * GEMM_LDS_STRIDE + lk]) = ra;
+  };
+
+  // Schedule (all slot and buffer indices compile-time, so each step is straight-line code and
+  // the loads of a slot are waited for only when that slot is stored): step k stores slot
+  // (k + 1) % S into LDS buffer (k + 1) % 2, refills slot k % S with step k + S and multiplies
+  // buffer k % 2.  K / 64 is a multiple of S (checked by the host).
+  const int nk = g.K / GEMM_BK;
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
-        *reinterpret_cast<uint4*>(&Bs[cur ^ 1][b][lr * GEMM_LDS_STRIDE + lk]) = rb[b];
+  for (int s = 0; s < S; ++s) load_step(s, ra[s], rb[s]);
+  store_step(0, ra[0], rb[0]);
+  __syncthreads();
+  for (int kb = 0; kb < nk - S; kb += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      store_step((s + 1) & 1, ra[(s + 1) % S], rb[(s + 1) % S]);
+      load_step(kb + s + S, ra[s], rb[s]);
+      mma_step(s & 1);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (s + 1 < S) store_step((s + 1) & 1, ra[s + 1], rb[s + 1]);
+    mma_step(s & 1);
+    __syncthreads();
+  }
+
+  if (KG == 2) {
+    // waves 2/3 hand their half-K sums to waves 0/1 through LDS (the last loop step synced)
+    float* red = reinterpret_cast<float*>(&As[0][0]);
+    if (wk == 1) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) red[(wn * 16 + j) * 64 + lane] = acc[0][j];
     }
     __syncthreads();
-    cur ^= 1;
+    if (wk == 1) return;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[0][j] += red[(wn * 16 + j) * 64 + lane];
   }
 
   // epilogue: acc[j] is C[row][col] with row = 8*(j/4) + 4*(lane/32) + j%4, col = lane%32
@@ -205,157 +266,186 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
       g.C[(size_t)row * g.ldc + col] = f32_to_bf16(v);
     }
   }
+  if (EPI == EPI_STORE && g.Vt != nullptr && n_base >= g.n1) {
+    // V^T for the prefill attention: accumulator elements 4 jg .. 4 jg + 3 are 4 consecutive rows
+    bf16_t* vt = g.Vt + (size_t)(col - g.n1) * g.ldvt;
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+      const int row = m_base + wm * 32 + 8 * jg + 4 * (lane >> 5);
+      if (row + 3 < g.M) {
+        uint2 w;
+        w.x = pack_bf16x2(acc[0][4 * jg], acc[0][4 * jg + 1]);
+        w.y = pack_bf16x2(acc[0][4 * jg + 2], acc[0][4 * jg + 3]);
+        *reinterpret_cast<uint2*>(vt + row) = w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (row + e < g.M) vt[row + e] = f32_to_bf16(acc[0][4 * jg + e]);
+      }
+    }
+  }
 }
 
 // --------------------------------------------------------------------- causal attention
-// Flash-style causal GQA attention of one kv head over 32 query positions per workgroup
-// (2 waves: query heads 2h and 2h+1 share every K/V tile).  Per 32-key tile: S = Q K^T with
-// v_mfma_f32_32x32x16_bf16 (q and k are bf16, so the fp32 scores are exact up to accumulation
-// order), online softmax in fp32 on the accumulator layout, then O += P V where P is split into
-// bf16 hi + lo parts (two MFMAs) so the weights keep ~16 bits more than bf16, close to the
-// reference's fp32 softmax (prefill_causal_attention_kernel, fused_prefill_kernels.inl:265-342).
+// Flash-style causal GQA attention (prefill_causal_attention_kernel,
+// fused_prefill_kernels.inl:265-342), one wave per (32 query positions, query head), keys in
+// tiles of 32, on v_mfma_f32_32x32x16_bf16:
+//   S^T = K Q^T      rows are keys, so every lane holds the 16 scores of ONE query (its lane
+//                    pair holds the other 16): the softmax max needs one lane swap per tile and
+//                    the row sum none until the end;
+//   O^T += V^T P^T   P^T is the score accumulator itself.  K tile row r carries key
+//                    att_key_perm(r) (bits 2 and 3 of r swapped), which makes accumulator element
+//                    j of lane l the key 16 (j / 8) + 8 (l / 32) + j % 8: exactly the B-operand
+//                    layout of two 16-key MFMA steps, so P never leaves the registers.
+// q and k are bf16, so the fp32 scores are exact up to accumulation order; the softmax is fp32
+// and P enters the MFMA as bf16 hi + lo parts (two MFMAs), keeping ~16 more bits than bf16,
+// close to the reference's fp32 weights.  V^T (dims x keys) is written by the QKV GEMM epilogue.
 #define ATT_KT 32
-#define ATT_KSTR 136     // K tile row stride (bf16): 128 + 8
-#define ATT_VSTR 40      // transposed V tile row stride (bf16): 32 + 8
-#define ATT_PSTR 36      // P tile row stride (fp32): 32 + 4
 
-__global__ void __launch_bounds__(128) pf_attn_kernel(MqDecodeParams p, int layer,
-                                                      const bf16_t* __restrict__ qkv,
-                                                      bf16_t* __restrict__ att, int n) {
-  __shared__ __align__(16) bf16_t Ks[ATT_KT * ATT_KSTR];
-  __shared__ __align__(16) bf16_t Vt[MQ_D * ATT_VSTR];
-  __shared__ __align__(16) float Ps[2][32 * ATT_PSTR];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int h = blockIdx.y, qh = 2 * h + wave;
-  const int q0 = blockIdx.x * 32;
-  const int fr = lane & 31, fk = (lane >> 5) * 8;
+MQ_DEV int att_key_perm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+__global__ void __launch_bounds__(64) pf_attn_kernel(MqDecodeParams p, int layer,
+                                                     const bf16_t* __restrict__ qkv,
+                                                     const bf16_t* __restrict__ vt, int ldvt,
+                                                     bf16_t* __restrict__ att, int n) {
+  const int lane = threadIdx.x;
+  const int qh = blockIdx.y, h = qh >> 1;          // q heads 2h and 2h+1 share kv head h
+  const int qb = gridDim.x - 1 - blockIdx.x;       // longest query blocks first
+  const int q0 = qb * 32;
+  const int fr = lane & 31, hh = lane >> 5;
+  const int q = q0 + fr;                           // this lane's query position
   const bf16_t* Kc = p.kc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
-  const bf16_t* Vc = p.vc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
+  const bf16_t* Vt = vt + (size_t)h * MQ_D * ldvt;
 
-  // Q fragments: query row q0 + lane%32, dims 16s + 8*(lane/32) .. +8
+  // Q^T operand: query q, dims 16 s + 8 hh .. + 8 (rows past n read row n - 1, never stored)
   mq_bf16x8 qf[8];
   {
-    const int qr = q0 + fr;
-    const bf16_t* src = qkv + (size_t)(qr < n ? qr : n - 1) * MQ_QKV + qh * MQ_D + fk;
+    const bf16_t* src = qkv + (size_t)min(q, n - 1) * MQ_QKV + qh * MQ_D + 8 * hh;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = as_bf16x8(qr < n ? ld16(src + 16 * s) : make_uint4(0, 0, 0, 0));
+    for (int s = 0; s < 8; ++s) qf[s] = as_bf16x8(ld16(src + 16 * s));
   }
+  // K operand: key att_key_perm(fr) of the tile, dims 16 s + 8 hh .. + 8
+  const int kr = att_key_perm(fr);
+  mq_bf16x8 kf[8];
+  auto load_k = [&](int k0) {
+    const bf16_t* src = Kc + (size_t)min(k0 + kr, n - 1) * MQ_D + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) kf[s] = as_bf16x8(ld16(src + 16 * s));
+  };
+
   mq_f32x16 o[4];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
     for (int j = 0; j < 16; ++j) o[nt][j] = 0.f;
-  float m[16], l[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    m[j] = -INFINITY;
-    l[j] = 0.f;
-  }
+  float m = -INFINITY, l = 0.f;
   const float scale = p.scale_log2;
-  const int q_last = min(n, q0 + 32) - 1;
-  float* P = Ps[wave];
-  for (int k0 = 0; k0 <= q_last; k0 += ATT_KT) {
-    // K tile row-major, V tile transposed (dim-major) into LDS; 128 threads x 4 x 16 bytes each
+  load_k(0);
+  for (int kt = 0; kt <= qb; ++kt) {
+    const int k0 = kt * ATT_KT;
+    // V^T operand: dim 32 nt + fr, keys k0 + 16 s + 8 hh .. + 8
+    uint4 vf[4][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int idx = t + 128 * i;          // 0..255: key idx/8, dim chunk (idx%8)*16 ... as 16B units
-      const int key = idx >> 3, dc = (idx & 7) * 16;
-      const int kk = k0 + key;
-      const bool ok = kk < n;
-      uint4 kv0 = ok ? ld16(Kc + (size_t)kk * MQ_D + dc) : make_uint4(0, 0, 0, 0);
-      uint4 kv1 = ok ? ld16(Kc + (size_t)kk * MQ_D + dc + 8) : make_uint4(0, 0, 0, 0);
-      uint4 vv0 = ok ? ld16(Vc + (size_t)kk * MQ_D + dc) : make_uint4(0, 0, 0, 0);
-      uint4 vv1 = ok ? ld16(Vc + (size_t)kk * MQ_D + dc + 8) : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(&Ks[key * ATT_KSTR + dc]) = kv0;
-      *reinterpret_cast<uint4*>(&Ks[key * ATT_KSTR + dc + 8]) = kv1;
-      const uint32_t vw[8] = {vv0.x, vv0.y, vv0.z, vv0.w, vv1.x, vv1.y, vv1.z, vv1.w};
+    for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        Vt[(dc + 2 * e) * ATT_VSTR + key] = (bf16_t)(vw[e] & 0xffffu);
-        Vt[(dc + 2 * e + 1) * ATT_VSTR + key] = (bf16_t)(vw[e] >> 16);
-      }
-    }
-    __syncthreads();
-    // S = Q K^T  (rows: queries, cols: keys)
+      for (int s = 0; s < 2; ++s)
+        vf[nt][s] = ld16(Vt + (size_t)(32 * nt + fr) * ldvt + k0 + 16 * s + 8 * hh);
     mq_f32x16 sacc;
 #pragma unroll
     for (int j = 0; j < 16; ++j) sacc[j] = 0.f;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const mq_bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(&Ks[fr * ATT_KSTR + 16 * s + fk]));
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[s], kf, sacc, 0, 0, 0);
-    }
-    // mask, online softmax (row j of this lane: query q0 + rowj, key k0 + lane%32)
-    const int key = k0 + fr;
+    for (int s = 0; s < 8; ++s) sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s], qf[s], sacc, 0, 0, 0);
+    if (kt < qb) load_k(k0 + ATT_KT);
+    // causal mask on the diagonal tile (the only tile holding keys > q or keys >= n)
+    const bool diag = kt == qb;
+    float sv[16];
+    float mloc = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int qrow = q0 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-      float sv = (key <= qrow && key < n) ? sacc[j] * scale : -INFINITY;
-      float mx = row16_max(sv);
-      mx = fmaxf(mx, xor_lane(mx, 16));
-      const float m_new = fmaxf(m[j], mx);
-      const float alpha = exp2f(m[j] - m_new);
-      const float pv = exp2f(sv - m_new);
-      float ps = row16_sum(pv);
-      ps += xor_lane(ps, 16);
-      l[j] = l[j] * alpha + ps;
-      m[j] = m_new;
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) o[nt][j] *= alpha;
-      P[(8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)) * ATT_PSTR + fr] = pv;
+      const int key = k0 + 16 * (j >> 3) + 8 * hh + (j & 7);
+      sv[j] = (!diag || key <= q) ? sacc[j] * scale : -INFINITY;
+      mloc = fmaxf(mloc, sv[j]);
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    // O += P V with P = hi + lo (bf16 each)
+    const float m_new = fmaxf(m, max_xor32(mloc));
+    const float alpha = exp2f(m - m_new);
+    m = m_new;
+    float ls = 0.f;
+    mq_bf16x8 phi[2], plo[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      float pr[8];
+    for (int j = 0; j < 16; ++j) {
+      const float pv = exp2f(sv[j] - m_new);
+      ls += pv;
+      const __bf16 hb = (__bf16)pv;
+      phi[j >> 3][j & 7] = hb;
+      plo[j >> 3][j & 7] = (__bf16)(pv - (float)hb);
+    }
+    l = l * alpha + ls;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pr[e] = P[fr * ATT_PSTR + 16 * s + fk + e];
-      mq_bf16x8 phi, plo;
+    for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const __bf16 hb = (__bf16)pr[e];
-        phi[e] = hb;
-        plo[e] = (__bf16)(pr[e] - (float)hb);
+      for (int j = 0; j < 16; ++j) o[nt][j] *= alpha;
+    if (diag && k0 + ATT_KT > n) {
+      // keys >= n: their weights are 0, but the V^T padding may hold anything (0 * NaN)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int kbase = k0 + 16 * s + 8 * hh;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          uint32_t w[4] = {vf[nt][s].x, vf[nt][s].y, vf[nt][s].z, vf[nt][s].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (kbase + 2 * e >= n) w[e] &= 0xffff0000u;
+            if (kbase + 2 * e + 1 >= n) w[e] &= 0x0000ffffu;
+          }
+          vf[nt][s] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
       }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
-        const mq_bf16x8 vf = as_bf16x8(
-            *reinterpret_cast<const uint4*>(&Vt[(nt * 32 + fr) * ATT_VSTR + 16 * s + fk]));
-        o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(phi, vf, o[nt], 0, 0, 0);
-        o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(plo, vf, o[nt], 0, 0, 0);
+        const mq_bf16x8 vb = as_bf16x8(vf[nt][s]);
+        o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, phi[s], o[nt], 0, 0, 0);
+        o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, plo[s], o[nt], 0, 0, 0);
       }
-    }
-    __syncthreads();
   }
-  // normalise and store bf16: O[row][dim] with dim = 32*nt + lane%32
+  // each lane of a pair summed its own 16 keys of every tile
+  l = sum_xor32(l);
+  if (q < n) {
+    const float inv = 1.0f / l;
+    bf16_t* dst = att + (size_t)q * MQ_QDIM + qh * MQ_D;
+    // O^T accumulator element j of tile nt: dim 32 nt + 8 (j / 4) + 4 hh + j % 4
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int qrow = q0 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-    if (qrow < n) {
-      const float inv = 1.0f / l[j];
+    for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        att[(size_t)qrow * MQ_QDIM + qh * MQ_D + nt * 32 + fr] = f32_to_bf16(o[nt][j] * inv);
-    }
+      for (int jg = 0; jg < 4; ++jg) {
+        uint2 w;
+        w.x = pack_bf16x2(o[nt][4 * jg] * inv, o[nt][4 * jg + 1] * inv);
+        w.y = pack_bf16x2(o[nt][4 * jg + 2] * inv, o[nt][4 * jg + 3] * inv);
+        *reinterpret_cast<uint2*>(dst + 32 * nt + 8 * jg + 4 * hh) = w;
+      }
   }
 }
 
 // -------------------------------------------------------------------------- host side
 static size_t pf_align(size_t v) { return (v + 255) / 256 * 256; }
 
+// V^T rows hold whole 32-key tiles
+static int pf_ldvt(int max_n) { return (max_n + 31) / 32 * 32; }
+
 size_t mq_prefill_workspace_bytes(int max_n) {
   if (max_n <= 0) return 0;
   const size_t n = (size_t)max_n;
   return pf_align(n * MQ_H * 2) * 2 + pf_align(n * MQ_QKV * 2) + pf_align(n * MQ_QDIM * 2) +
-         pf_align(n * MQ_I * 2);
+         pf_align(n * MQ_I * 2) + pf_align((size_t)MQ_KVDIM * pf_ldvt(max_n) * 2);
 }
 
 void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n) {
   b->max_n = max_n;
   if (max_n <= 0) {
-    b->h = b->xn = b->qkv = b->att = b->m = nullptr;
+    b->h = b->xn = b->qkv = b->att = b->m = b->vt = nullptr;
+    b->ldvt = 0;
     return;
   }
   const size_t n = (size_t)max_n;
@@ -364,13 +454,23 @@ void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n) {
   b->xn = reinterpret_cast<bf16_t*>(c);  c += pf_align(n * MQ_H * 2);
   b->qkv = reinterpret_cast<bf16_t*>(c); c += pf_align(n * MQ_QKV * 2);
   b->att = reinterpret_cast<bf16_t*>(c); c += pf_align(n * MQ_QDIM * 2);
-  b->m = reinterpret_cast<bf16_t*>(c);
+  b->m = reinterpret_cast<bf16_t*>(c);    c += pf_align(n * MQ_I * 2);
+  b->vt = reinterpret_cast<bf16_t*>(c);
+  b->ldvt = pf_ldvt(max_n);
 }
 
+// K must be a multiple of 256 and N of 64 (every Qwen3-0.6B projection is).  Tiles of 32 rows
+// are used when 64-row tiles would leave CUs idle (the N = 1024 GEMMs at M <= 1024).
 template <int EPI>
 static void gemm(const GemmArgs& g, hipStream_t s) {
-  dim3 grid(g.N / GEMM_BN, (g.M + GEMM_BM - 1) / GEMM_BM);
-  pf_gemm_kernel<EPI><<<grid, 256, 0, s>>>(g);
+  const int nt = g.N / GEMM_BN;
+  if constexpr (EPI != EPI_SWIGLU) {
+    if (nt * ((g.M + 63) / 64) < 256) {
+      pf_gemm_kernel<EPI, 32><<<dim3(nt, (g.M + 31) / 32), 256, 0, s>>>(g);
+      return;
+    }
+  }
+  pf_gemm_kernel<EPI, 64><<<dim3(nt, (g.M + 63) / 64), 256, 0, s>>>(g);
 }
 
 int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefillBuffers& b,
@@ -385,9 +485,11 @@ int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefi
     g.A = b.xn; g.lda = MQ_H;
     g.B0 = w.wq; g.B1 = w.wk; g.B2 = w.wv; g.n0 = MQ_QDIM; g.n1 = MQ_QDIM + MQ_KVDIM;
     g.C = b.qkv; g.ldc = MQ_QKV; g.M = n; g.N = MQ_QKV; g.K = MQ_H;
+    g.Vt = b.vt; g.ldvt = b.ldvt;
     gemm<EPI_STORE>(g, stream);
     pf_qk_norm_rope_kernel<<<dim3(n, MQ_NQ + MQ_NKV), 64, 0, stream>>>(p, l, b.qkv);
-    pf_attn_kernel<<<dim3((n + 31) / 32, MQ_NKV), 128, 0, stream>>>(p, l, b.qkv, b.att, n);
+    pf_attn_kernel<<<dim3((n + 31) / 32, MQ_NQ), 64, 0, stream>>>(p, l, b.qkv, b.vt, b.ldvt,
+                                                                  b.att, n);
     g = GemmArgs{};
     g.A = b.att; g.lda = MQ_QDIM;
     g.B0 = g.B1 = g.B2 = w.wo; g.n0 = g.n1 = MQ_H;
