@@ -22,6 +22,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 typedef __bf16 mq_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float mq_f32x16 __attribute__((ext_vector_type(16)));
 
@@ -304,16 +306,29 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
 
 MQ_DEV int att_key_perm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
-__global__ void __launch_bounds__(64) pf_attn_kernel(MqDecodeParams p, int layer,
-                                                     const bf16_t* __restrict__ qkv,
-                                                     const bf16_t* __restrict__ vt, int ldvt,
-                                                     bf16_t* __restrict__ att, int n) {
-  const int lane = threadIdx.x;
-  const int qh = blockIdx.y, h = qh >> 1;          // q heads 2h and 2h+1 share kv head h
-  const int qb = gridDim.x - 1 - blockIdx.x;       // longest query blocks first
+// A workgroup is one (query head, 32-query block); its blockDim.x / 64 waves (<= ATT_SPLIT) split
+// the block's key tiles into contiguous ranges and merge their (max, sum, O) partials through LDS
+// at the end, in wave order.  Query blocks are dispatched longest first (blockIdx.y = 0 is the
+// last block).  The kernel is held to 256 registers so that two waves share each SIMD: one
+// wave's softmax (VALU) runs while the other's MFMAs run.  K is loaded one tile ahead.
+#define ATT_SPLIT 4
+#ifndef ATT_P_SPLIT
+#define ATT_P_SPLIT 1
+#endif
+
+__global__ void __launch_bounds__(64 * ATT_SPLIT) __attribute__((amdgpu_waves_per_eu(2)))
+pf_attn_kernel(MqDecodeParams p, int layer, const bf16_t* __restrict__ qkv,
+               const bf16_t* __restrict__ vt, int ldvt, bf16_t* __restrict__ att, int n) {
+  __shared__ float red[ATT_SPLIT - 1][66][64];     // waves 1.. : o (64 per lane), m, l
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // kv head h = blockIdx.x % 8 is the XCD the workgroup runs on (workgroups are dealt to the 8
+  // XCDs round robin and gridDim.x = 16), so each XCD's L2 holds the K/V^T of one kv head only
+  const int h = blockIdx.x & 7, qh = 2 * h + (blockIdx.x >> 3);   // q heads 2h, 2h+1 share h
+  const int qb = gridDim.y - 1 - blockIdx.y;
   const int q0 = qb * 32;
   const int fr = lane & 31, hh = lane >> 5;
   const int q = q0 + fr;                           // this lane's query position
+  const int t0 = (qb + 1) * wave / nw, t1 = (qb + 1) * (wave + 1) / nw;   // key tiles of this wave
   const bf16_t* Kc = p.kc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
   const bf16_t* Vt = vt + (size_t)h * MQ_D * ldvt;
 
@@ -325,12 +340,13 @@ __global__ void __launch_bounds__(64) pf_attn_kernel(MqDecodeParams p, int layer
     for (int s = 0; s < 8; ++s) qf[s] = as_bf16x8(ld16(src + 16 * s));
   }
   // K operand: key att_key_perm(fr) of the tile, dims 16 s + 8 hh .. + 8
-  const int kr = att_key_perm(fr);
-  mq_bf16x8 kf[8];
-  auto load_k = [&](int k0) {
-    const bf16_t* src = Kc + (size_t)min(k0 + kr, n - 1) * MQ_D + 8 * hh;
+  const bf16_t* ksrc = Kc + (size_t)att_key_perm(fr) * MQ_D + 8 * hh;
+  const int kmax = n - 1 - att_key_perm(fr);       // keys past n - 1 read row n - 1
+  uint4 kf[8];
+  auto load_k = [&](int kt) {
+    const bf16_t* src = ksrc + (size_t)min(kt * ATT_KT, kmax) * MQ_D;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) kf[s] = as_bf16x8(ld16(src + 16 * s));
+    for (int s = 0; s < 8; ++s) kf[s] = ld16(src + 16 * s);
   };
 
   mq_f32x16 o[4];
@@ -338,10 +354,12 @@ __global__ void __launch_bounds__(64) pf_attn_kernel(MqDecodeParams p, int layer
   for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
     for (int j = 0; j < 16; ++j) o[nt][j] = 0.f;
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY, l = 0.f;                    // running max (scaled, log2 units) and sum
   const float scale = p.scale_log2;
-  load_k(0);
-  for (int kt = 0; kt <= qb; ++kt) {
+  // One key tile.  DIAG: the diagonal tile, the only one holding keys > q or keys >= n (its
+  // masked variant is compiled separately so the other tiles carry no per-score selects).
+  auto tile = [&](int kt, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
     const int k0 = kt * ATT_KT;
     // V^T operand: dim 32 nt + fr, keys k0 + 16 s + 8 hh .. + 8
     uint4 vf[4][2];
@@ -354,37 +372,46 @@ __global__ void __launch_bounds__(64) pf_attn_kernel(MqDecodeParams p, int layer
 #pragma unroll
     for (int j = 0; j < 16; ++j) sacc[j] = 0.f;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s], qf[s], sacc, 0, 0, 0);
-    if (kt < qb) load_k(k0 + ATT_KT);
-    // causal mask on the diagonal tile (the only tile holding keys > q or keys >= n)
-    const bool diag = kt == qb;
-    float sv[16];
-    float mloc = -INFINITY;
+    for (int s = 0; s < 8; ++s)
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[s]), qf[s], sacc, 0, 0, 0);
+    if (kt + 1 < t1) load_k(kt + 1);
+    float raw[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int key = k0 + 16 * (j >> 3) + 8 * hh + (j & 7);
-      sv[j] = (!diag || key <= q) ? sacc[j] * scale : -INFINITY;
-      mloc = fmaxf(mloc, sv[j]);
+      raw[j] = (!DIAG || key <= q) ? sacc[j] : -INFINITY;
     }
-    const float m_new = fmaxf(m, max_xor32(mloc));
-    const float alpha = exp2f(m - m_new);
+    float mloc = fmaxf(raw[0], raw[1]);
+#pragma unroll
+    for (int j = 2; j < 16; j += 2) mloc = fmaxf(mloc, fmaxf(raw[j], raw[j + 1]));
+    // max(raw) * scale == max(raw * scale): rounding is monotonic and scale > 0
+    const float m_new = fmaxf(m, max_xor32(mloc) * scale);
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
     m = m_new;
     float ls = 0.f;
-    mq_bf16x8 phi[2], plo[2];
+    mq_bf16x8 phi[2];
+#if ATT_P_SPLIT
+    mq_bf16x8 plo[2];
+#endif
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const float pv = exp2f(sv[j] - m_new);
+      const float pv = __builtin_amdgcn_exp2f(fmaf(raw[j], scale, -m_new));
       ls += pv;
       const __bf16 hb = (__bf16)pv;
       phi[j >> 3][j & 7] = hb;
+#if ATT_P_SPLIT
       plo[j >> 3][j & 7] = (__bf16)(pv - (float)hb);
+#endif
     }
     l = l * alpha + ls;
+    // rescale only when some lane's max moved (alpha == 1 leaves o unchanged bit for bit)
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+      for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) o[nt][j] *= alpha;
-    if (diag && k0 + ATT_KT > n) {
+        for (int j = 0; j < 16; ++j) o[nt][j] *= alpha;
+    }
+    if (DIAG && k0 + ATT_KT > n) {
       // keys >= n: their weights are 0, but the V^T padding may hold anything (0 * NaN)
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
@@ -407,8 +434,45 @@ __global__ void __launch_bounds__(64) pf_attn_kernel(MqDecodeParams p, int layer
       for (int nt = 0; nt < 4; ++nt) {
         const mq_bf16x8 vb = as_bf16x8(vf[nt][s]);
         o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, phi[s], o[nt], 0, 0, 0);
+#if ATT_P_SPLIT
         o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, plo[s], o[nt], 0, 0, 0);
+#endif
       }
+  };
+  if (t0 < t1) load_k(t0);
+  const int tend = min(t1, qb);                    // tiles below the diagonal
+  for (int kt = t0; kt < tend; ++kt) tile(kt, std::false_type{});
+  if (t1 == qb + 1) tile(qb, std::true_type{});
+  // merge the key ranges: wave 0 rescales every partial to the common max (a wave with no tiles
+  // has m = -inf and contributes 0; the wave holding the diagonal tile always has a finite m)
+  if (wave > 0) {
+    float* r = &red[wave - 1][0][lane];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) r[(16 * nt + j) * 64] = o[nt][j];
+    r[64 * 64] = m;
+    r[65 * 64] = l;
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  float mt = m;
+  for (int w = 1; w < nw; ++w) mt = fmaxf(mt, red[w - 1][64][lane]);
+  {
+    const float a = __builtin_amdgcn_exp2f(m - mt);
+    l *= a;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) o[nt][j] *= a;
+  }
+  for (int w = 1; w < nw; ++w) {
+    const float a = __builtin_amdgcn_exp2f(red[w - 1][64][lane] - mt);
+    l = fmaf(red[w - 1][65][lane], a, l);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) o[nt][j] = fmaf(red[w - 1][16 * nt + j][lane], a, o[nt][j]);
   }
   // each lane of a pair summed its own 16 keys of every tile
   l = sum_xor32(l);
@@ -488,8 +552,8 @@ int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefi
     g.Vt = b.vt; g.ldvt = b.ldvt;
     gemm<EPI_STORE>(g, stream);
     pf_qk_norm_rope_kernel<<<dim3(n, MQ_NQ + MQ_NKV), 64, 0, stream>>>(p, l, b.qkv);
-    pf_attn_kernel<<<dim3((n + 31) / 32, MQ_NQ), 64, 0, stream>>>(p, l, b.qkv, b.vt, b.ldvt,
-                                                                  b.att, n);
+    pf_attn_kernel<<<dim3(MQ_NQ, (n + 31) / 32), 64 * ATT_SPLIT, 0, stream>>>(
+        p, l, b.qkv, b.vt, b.ldvt, b.att, n);
     g = GemmArgs{};
     g.A = b.att; g.lda = MQ_QDIM;
     g.B0 = g.B1 = g.B2 = w.wo; g.n0 = g.n1 = MQ_H;

@@ -106,6 +106,48 @@ def test_prefill_vs_decode_only_next_token(small):
             assert t_dec == t_pf
 
 
+def _attention_fp32(q, k, v):
+    """Causal GQA attention in fp32 on the CPU: q [n, 16, 128], k/v [8, n, 128] -> [n, 16, 128]."""
+    n = q.shape[0]
+    out = torch.empty(n, 16, 128)
+    mask = torch.ones(n, n, dtype=torch.bool).triu(1)
+    for qh in range(16):
+        s = (q[:, qh] @ k[qh // 2].T) / 128 ** 0.5
+        s.masked_fill_(mask, float("-inf"))
+        out[:, qh] = torch.softmax(s, dim=-1) @ v[qh // 2]
+    return out
+
+
+@pytest.mark.parametrize("n", [33, 512, 2000])
+def test_prefill_attention_kernel_vs_fp32(small, n):
+    """The causal attention kernel alone: the last layer's bf16 output against fp32 attention of
+    the same bf16 q (rotated, from the q|k|v buffer) and K/V cache rows.  Bound: one bf16 ulp of
+    the result (the output rounding) plus 2e-3 x max |v| for the fp32 reductions and the bf16
+    hi + lo split of the softmax weights."""
+    if n > 512:
+        dec, _, sp, _ = build_pair(1, 4096, n + 8, seed=5, norm_jitter=0.1, max_prefill=n,
+                                   oracle=False)
+    else:
+        dec, _, sp, _ = small
+    layer = sp["num_layers"] - 1
+    dec.reset()
+    dec.prefill_step(make_tokens(n, sp["vocab_size"], seed=40 + n))
+    torch.cuda.synchronize()
+    bufs = dec.debug_prefill_buffers(n)
+    q = bufs["qkv"][:, :2048].float().cpu().view(n, 16, 128)
+    k = dec.k_cache[layer, :, :n].float().cpu()
+    v = dec.v_cache[layer, :, :n].float().cpu()
+    got = bufs["att"].float().cpu().view(n, 16, 128)
+    ref = _attention_fp32(q, k, v)
+    d = (got - ref).abs()
+    bound = _bf16_ulp(ref) + 2e-3 * float(v.abs().max())
+    print(f"attention n={n}: max |d| {float(d.max()):.3e}, max |d| / ulp "
+          f"{float((d / _bf16_ulp(ref)).max()):.2f}, bit-equal to bf16(ref) "
+          f"{float((got == ref.to(torch.bfloat16).float()).float().mean()):.4f}")
+    assert (d <= bound).all()
+    dec.check()
+
+
 def test_prefill_errors(small):
     dec, _, sp, _ = small
     with pytest.raises(RuntimeError):
