@@ -157,6 +157,16 @@ int mq_decoder_check(mq_decoder* dec, void* stream);
 int mq_prefill(mq_decoder* dec, const int32_t* d_tokens, int n, int32_t* d_token_out,
                float* d_logits, void* stream);
 
+/* Prefill with caller-supplied embedding rows: as mq_prefill, but rows
+ * [embeds_start, embeds_start + embeds_len) of the input take d_embeds (bf16
+ * [embeds_len, 1024], e.g. audio-tower outputs) instead of the token embeddings.
+ * Replaces prefill_asr (bindings_prefill.cpp:835-955, bindings_fused_prefill.cpp:286-330) and
+ * prefill_patch_audio_kernel (fused_prefill_kernels.inl:28-45); errors as bindings_prefill.cpp:
+ * 838-859 (embeds_len > 0, 0 <= embeds_start, embeds_start + embeds_len <= n). */
+int mq_prefill_embeds(mq_decoder* dec, const int32_t* d_tokens, int n, const void* d_embeds,
+                      int embeds_start, int embeds_len, int32_t* d_token_out, float* d_logits,
+                      void* stream);
+
 /* Debug hook: device addresses (inside the workspace) of the prefill buffers of the last
  * prefill: out5 = {h [n,H], xn [n,H], qkv [n,Hq*D+2*Hkv*D], att [n,Hq*D], mlp [n,I]}, bf16. */
 int mq_debug_prefill_buffers(const mq_decoder* dec, void** out5);

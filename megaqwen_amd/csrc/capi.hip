@@ -350,6 +350,26 @@ int mq_prefill(mq_decoder* dec, const int32_t* d_tokens, int n, int32_t* d_token
   return MQ_OK;
 }
 
+int mq_prefill_embeds(mq_decoder* dec, const int32_t* d_tokens, int n, const void* d_embeds,
+                      int embeds_start, int embeds_len, int32_t* d_token_out, float* d_logits,
+                      void* stream) {
+  if (dec == nullptr || d_tokens == nullptr || d_token_out == nullptr || d_embeds == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "decoder, token and embedding pointers must be non-NULL");
+  if (n > dec->max_prefill) return fail(MQ_ERR_INVALID_ARG, "Prefill sequence length exceeds maximum");
+  if (n <= 0) return fail(MQ_ERR_INVALID_ARG, "Empty input sequence");
+  if (embeds_len <= 0) return fail(MQ_ERR_INVALID_ARG, "audio_embeds must have audio_len > 0");
+  if (embeds_start < 0 || embeds_start + embeds_len > n)
+    return fail(MQ_ERR_INVALID_ARG, "Invalid audio_start_idx/audio_len for the given seq_len");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = mq_launch_prefill(dec->p, dec->host_layers.data(), dec->pf, d_tokens, n, d_token_out,
+                             d_logits, dec->grid, s, static_cast<const bf16_t*>(d_embeds),
+                             embeds_start, embeds_len);
+  if (rc != 0) return fail(MQ_ERR_HIP, "prefill launch failed (%d)", rc);
+  if (mq_launch_fill_state(dec->p.st, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
+  dec->pos = n;
+  return MQ_OK;
+}
+
 int mq_debug_prefill_buffers(const mq_decoder* dec, void** out5) {
   if (dec == nullptr || out5 == nullptr) return fail(MQ_ERR_INVALID_ARG, "NULL argument");
   out5[0] = dec->pf.h;

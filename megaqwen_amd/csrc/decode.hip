@@ -53,9 +53,9 @@ static_assert(MQ_SYNC_WAVE == MQ_CWAVES && MQ_CWAVES + 1 == MQ_WAVES, "one sync 
 #define LDS_HID 4608      // [1024] the layer input (residual of the attention block)
 #define LDS_A 5632        // [1024] a = layer input + attention block output (MLP residual)
 #define LDS_ATTH 0        // [256]  merged attention output of the group's two query heads
-#define LDS_AROW 6656     // [MQ_CWAVES * 4][256] attention: unnormalised p.V of each position row
-#define LDS_AL (LDS_AROW + MQ_CWAVES * 4 * 256)   // [MQ_CWAVES * 4][2] row sums of p
-#define MQ_LDS_FLOATS (LDS_AL + MQ_CWAVES * 4 * 2)
+#define LDS_AROW 6656     // [MQ_CWAVES][256] attention: unnormalised p.V of each compute wave
+#define LDS_AL (LDS_AROW + MQ_CWAVES * 256)   // [MQ_CWAVES][2] sums of p of each compute wave
+#define MQ_LDS_FLOATS (LDS_AL + MQ_CWAVES * 2)
 
 // Balanced contiguous row range of workgroup `wg` out of `G` for an `n`-row matrix.
 MQ_DEV void row_range(int n, int wg, int G, int& r0, int& nr) {
@@ -468,43 +468,52 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
       m0 = n0;
       m1 = n1;
     }
-    // each position row leaves its p.V and sum of p in LDS; rows and waves are combined in the
-    // merge below (cheaper than reducing across rows in registers)
-    float* arow = lds + LDS_AROW + (wave * 4 + g) * 256;
+    // sum the wave's 4 position rows (lane groups of 16 share the wave's max) with row swaps,
+    // so that the merge below reads one row per wave
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      arow[sub * 8 + e] = acc0[e];
-      arow[MQ_D + sub * 8 + e] = acc1[e];
+      acc0[e] = sum_xor32(sum_xor16(acc0[e]));
+      acc1[e] = sum_xor32(sum_xor16(acc1[e]));
     }
-    if (sub == 0) {
-      lds[LDS_AL + (wave * 4 + g) * 2 + 0] = l0;
-      lds[LDS_AL + (wave * 4 + g) * 2 + 1] = l1;
+    l0 = sum_xor32(sum_xor16(l0));
+    l1 = sum_xor32(sum_xor16(l1));
+    if (g == 0) {
+      float4* arow = reinterpret_cast<float4*>(lds + LDS_AROW + wave * 256 + sub * 8);
+      arow[0] = make_float4(acc0[0], acc0[1], acc0[2], acc0[3]);
+      arow[1] = make_float4(acc0[4], acc0[5], acc0[6], acc0[7]);
+      arow[MQ_D / 4] = make_float4(acc1[0], acc1[1], acc1[2], acc1[3]);
+      arow[MQ_D / 4 + 1] = make_float4(acc1[4], acc1[5], acc1[6], acc1[7]);
     }
     if (lane == 0) {
       wml[wave * 4 + 0] = m0;
       wml[wave * 4 + 1] = m1;
+      lds[LDS_AL + wave * 2 + 0] = l0;
+      lds[LDS_AL + wave * 2 + 1] = l1;
     }
   }
   __syncthreads();
-  // merge the compute waves' rows (every item has at least one valid position, so M is finite)
+  // merge the compute waves (every item has at least one valid position, so M is finite); all
+  // LDS reads are issued up front, waves past nwaves are masked by selects (their LDS is stale)
   if (tid() < 256) {
     const int j = tid() >> 7;
+    float mw[MQ_CWAVES], ow[MQ_CWAVES], lw[MQ_CWAVES];
+#pragma unroll
+    for (int w8 = 0; w8 < MQ_CWAVES; ++w8) {
+      mw[w8] = wml[w8 * 4 + j];
+      ow[w8] = lds[LDS_AROW + w8 * 256 + tid()];
+      lw[w8] = lds[LDS_AL + w8 * 2 + j];
+    }
     float M = -INFINITY;
 #pragma unroll
     for (int w8 = 0; w8 < MQ_CWAVES; ++w8)
-      if (w8 < nwaves) M = fmaxf(M, wml[w8 * 4 + j]);
+      if (w8 < nwaves) M = fmaxf(M, mw[w8]);
     float o = 0.f, L = 0.f;
 #pragma unroll
     for (int w8 = 0; w8 < MQ_CWAVES; ++w8) {
-      if (w8 >= nwaves) break;
-      const float mw = wml[w8 * 4 + j];
-      const float f = mw == -INFINITY ? 0.f : exp2_fast(mw - M);
-      const float* ar = lds + LDS_AROW + w8 * 4 * 256 + tid();
-      const float* al = lds + LDS_AL + w8 * 4 * 2 + j;
-      const float ow = (ar[0] + ar[256]) + (ar[512] + ar[768]);
-      const float lw = (al[0] + al[2]) + (al[4] + al[6]);
-      o = fmaf(f, ow, o);
-      L = fmaf(f, lw, L);
+      const bool use = w8 < nwaves && mw[w8] != -INFINITY;
+      const float f = use ? exp2_fast(mw[w8] - M) : 0.f;
+      o = use ? fmaf(f, ow[w8], o) : o;
+      L = use ? fmaf(f, lw[w8], L) : L;
     }
     ored[tid()] = o;
     if ((tid() & 127) == 0) {

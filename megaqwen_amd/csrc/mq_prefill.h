@@ -17,6 +17,9 @@ struct MqPrefillBuffers {
 size_t mq_prefill_workspace_bytes(int max_n);
 void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n);
 // `host_layers` is the host copy of the device layer table p.layers.
+// `patch` (optional, bf16 [patch_len, H]) replaces the embedding rows
+// [patch_start, patch_start + patch_len), which must lie inside [0, n).
 int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* host_layers,
                       const MqPrefillBuffers& b, const int32_t* tokens, int n, int32_t* tok_out,
-                      float* logits, int grid, hipStream_t stream);
+                      float* logits, int grid, hipStream_t stream, const bf16_t* patch = nullptr,
+                      int patch_start = 0, int patch_len = 0);

@@ -34,13 +34,20 @@ MQ_DEV uint32_t pack_bf16x2(float a, float b) {
 }
 
 // ------------------------------------------------------------------------- row kernels
+// Embedding gather (prefill_embed_kernel, fused_prefill_kernels.inl:3-20); rows
+// [patch_start, patch_start + patch_len) take the caller's bf16 rows instead (the audio span of
+// prefill_patch_audio_kernel, fused_prefill_kernels.inl:28-45, fused into the gather).
 __global__ void __launch_bounds__(128) pf_embed_kernel(const bf16_t* __restrict__ embed,
                                                        const int32_t* __restrict__ tokens,
-                                                       bf16_t* __restrict__ h) {
+                                                       bf16_t* __restrict__ h,
+                                                       const bf16_t* __restrict__ patch,
+                                                       int patch_start, int patch_len) {
   const int row = blockIdx.x;
-  const int tok = tokens[row];
+  const int pr = row - patch_start;
+  const bf16_t* src = (pr >= 0 && pr < patch_len) ? patch + (size_t)pr * MQ_H
+                                                  : embed + (size_t)tokens[row] * MQ_H;
   reinterpret_cast<uint4*>(h + (size_t)row * MQ_H)[threadIdx.x] =
-      reinterpret_cast<const uint4*>(embed + (size_t)tok * MQ_H)[threadIdx.x];
+      reinterpret_cast<const uint4*>(src)[threadIdx.x];
 }
 
 // y = bf16(x * rsqrt(mean(x^2) + eps) * w) for one 1024-wide row per workgroup
@@ -539,9 +546,12 @@ static void gemm(const GemmArgs& g, hipStream_t s) {
 
 int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefillBuffers& b,
                       const int32_t* tokens, int n, int32_t* tok_out, float* logits, int grid,
-                      hipStream_t stream) {
+                      hipStream_t stream, const bf16_t* patch, int patch_start, int patch_len) {
   if (n <= 0 || n > b.max_n || n > p.max_seq) return -3;
-  pf_embed_kernel<<<n, 128, 0, stream>>>(p.embed, tokens, b.h);
+  if (patch != nullptr && (patch_len <= 0 || patch_start < 0 || patch_start + patch_len > n))
+    return -3;
+  if (patch == nullptr) patch_len = 0;
+  pf_embed_kernel<<<n, 128, 0, stream>>>(p.embed, tokens, b.h, patch, patch_start, patch_len);
   for (int l = 0; l < p.num_layers; ++l) {
     const MqLayerW& w = hl[l];
     pf_rmsnorm_kernel<<<n, 128, 0, stream>>>(b.h, w.in_ln, b.xn);

@@ -296,6 +296,43 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
                                         _stream_ptr()))
         return int(self._tok[1].item())
 
+    def prefill_asr(self, input_token_ids, audio_embeds, audio_start_idx: int, *,
+                    return_logits: bool = False):
+        """Prefill whose embedding rows [audio_start_idx, audio_start_idx + audio_len) are the
+        caller's bf16 `audio_embeds` [audio_len, 1024] (bindings_prefill.cpp:835-955); returns
+        the greedy next token (with the last position's fp32 logits if return_logits) and sets
+        position = n.  Errors as the reference's checks."""
+        toks = torch.as_tensor(input_token_ids).reshape(-1)
+        n = int(toks.numel())
+        if n > self.max_prefill_len:
+            raise RuntimeError("Prefill sequence length exceeds maximum")
+        if n == 0:
+            raise RuntimeError("Empty input sequence")
+        if (not isinstance(audio_embeds, torch.Tensor) or not audio_embeds.is_cuda
+                or audio_embeds.dtype != torch.bfloat16 or audio_embeds.dim() != 2):
+            raise RuntimeError("audio_embeds must be a CUDA bfloat16 2D tensor [audio_len, hidden_size]")
+        audio_len, hidden = int(audio_embeds.shape[0]), int(audio_embeds.shape[1])
+        if hidden != 1024:
+            raise RuntimeError("audio_embeds hidden_size mismatch with compiled megakernel spec: "
+                               f"expected=1024, got={hidden}")
+        if audio_len <= 0:
+            raise RuntimeError("audio_embeds must have audio_len > 0")
+        start = int(audio_start_idx)
+        if start < 0 or start + audio_len > n:
+            raise RuntimeError("Invalid audio_start_idx/audio_len for the given seq_len")
+        if int(toks.min()) < 0 or int(toks.max()) >= self.vocab_size:
+            raise ValueError("token id outside the vocabulary")
+        d = toks.to(device=self._tok.device, dtype=torch.int32).contiguous()
+        emb = audio_embeds.contiguous()
+        if return_logits and self._logits is None:
+            self._logits = torch.empty(self.vocab_size, dtype=torch.float32, device=self._tok.device)
+        lg = self._logits.data_ptr() if return_logits else None
+        _lib.check(self._lib.mq_prefill_embeds(self._h, d.data_ptr(), n, emb.data_ptr(), start,
+                                               audio_len, self._tok.data_ptr() + 4, lg,
+                                               _stream_ptr()))
+        tok = int(self._tok[1].item())
+        return (tok, self._logits.clone()) if return_logits else tok
+
     def prefill_step_with_logits(self, input_token_ids):
         toks = torch.as_tensor(input_token_ids).reshape(-1)
         if self._logits is None:

@@ -164,9 +164,12 @@ class OracleModel:
         return (tok, logits) if return_logits else tok
 
     # ----------------------------------------------------------------- prefill
-    def prefill(self, tokens, return_logits: bool = True):
+    def prefill(self, tokens, return_logits: bool = True, embeds=None, embeds_start: int = 0):
         """Prefill of `tokens` at positions 0..n-1 (fused_prefill_launch.inl:245-657).
-        Writes K/V rows 0..n-1 and sets position = n (bindings_prefill.cpp:731-833)."""
+        Writes K/V rows 0..n-1 and sets position = n (bindings_prefill.cpp:731-833).
+        `embeds` [m, H] (bf16 values) replace the embedding rows [embeds_start, embeds_start + m)
+        (prefill_asr, bindings_prefill.cpp:835-955; prefill_patch_audio_kernel,
+        fused_prefill_kernels.inl:28-45)."""
         toks = torch.as_tensor(tokens, dtype=torch.long).reshape(-1)
         n = int(toks.numel())
         if n == 0:
@@ -175,6 +178,11 @@ class OracleModel:
             raise RuntimeError("Prefill sequence length exceeds maximum")
         R = self._r
         h = self.embed[toks].clone()                          # [n, H]
+        if embeds is not None:
+            e = torch.as_tensor(embeds).float().reshape(-1, h.shape[1])
+            if e.shape[0] <= 0 or embeds_start < 0 or embeds_start + e.shape[0] > n:
+                raise RuntimeError("Invalid audio_start_idx/audio_len for the given seq_len")
+            h[embeds_start:embeds_start + e.shape[0]] = e
         c, s = self.cos[:n].unsqueeze(1), self.sin[:n].unsqueeze(1)
         causal = torch.ones(n, n, dtype=torch.bool).tril()
         for li, w in enumerate(self.layers):

@@ -19,7 +19,7 @@ from megaqwen_amd.decoder import MegakernelDecoder
 from megaqwen_amd.rope import build_rope_tables
 from megaqwen_amd.synthetic import make_tokens
 from oracle.ref_cpu import rms_norm
-from tests.helpers import build_pair, to_cuda
+from tests.helpers import build_pair, to_cuda, top2_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -175,6 +175,26 @@ def test_op_lm_head_matches_rmsnorm_oracle(pair):
     dec.op_lm_head(x.cuda(), logits=logits)
     ref = w["embed_weight"].float() @ rms_norm(x.float(), w["final_norm_weight"].float())
     assert float((logits.cpu() - ref).abs().max()) < 1e-4
+
+
+def test_quality_harness_against_oracle(pair):
+    """quality_metrics.py's megakernel flow on the HIP decoder: KL(P_oracle || P_decoder) of the
+    last-position logits and argmax agreement over five prompts (the reference records KL 6e-4
+    and 100% argmax against HuggingFace, experiments/RESULTS.md:66)."""
+    from megaqwen_amd.quality import evaluate
+    dec, orc, sp, _ = pair
+    prompts = [make_tokens(k, sp["vocab_size"], seed=60 + k).tolist() for k in (3, 5, 8, 13, 21)]
+    refs = []
+    for ids in prompts:
+        orc.reset()
+        for t in ids[:-1]:
+            orc.decode_step(t)
+        refs.append(orc.decode_step(ids[-1])[1])
+    r = evaluate("hip", dec, prompts, refs)
+    print(f"quality: KL {r.kl_div:.3e}, argmax {r.argmax_match:.0%}")
+    # argmax must agree wherever the oracle's top-2 margin exceeds twice the 2e-2 logit bound
+    safe = sum(top2_margin(lg) > 4e-2 for lg in refs)
+    assert r.kl_div < 1e-4 and r.argmax_match >= safe / len(prompts)
 
 
 @pytest.mark.parametrize("kind", ["decode", "prefill"])

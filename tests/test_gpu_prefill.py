@@ -148,6 +148,50 @@ def test_prefill_attention_kernel_vs_fp32(small, n):
     dec.check()
 
 
+def test_prefill_asr_embedding_patch(small):
+    """prefill_asr (bindings_prefill.cpp:835-955): the patched prefill against the oracle's
+    patched prefill at the prefill tolerances; patching with the span's own token embeddings
+    reproduces prefill_step bit for bit; the K/V rows before the span are bit-identical to a plain
+    prefill (causality); the reference's argument errors."""
+    dec, orc, sp, _ = small
+    n, a, m = 40, 7, 12
+    toks = make_tokens(n, sp["vocab_size"], seed=77)
+    audio = (torch.randn(m, 1024, generator=torch.Generator().manual_seed(5)) * 0.05).to(torch.bfloat16)
+    dec.reset()
+    t_plain = dec.prefill_step(toks)
+    kp, vp = dec.k_cache.clone(), dec.v_cache.clone()
+    dec.reset()
+    assert dec.prefill_asr(toks, dec.embed_weight[toks[a:a + m].cuda()], a) == t_plain
+    assert torch.equal(dec.k_cache, kp) and torch.equal(dec.v_cache, vp)
+    dec.reset()
+    orc.reset()
+    tok = dec.prefill_asr(toks, audio.cuda(), a)
+    otok, olg = orc.prefill(toks, embeds=audio.float(), embeds_start=a)
+    assert dec.position() == n
+    assert torch.equal(dec.k_cache[:, :, :a], kp[:, :, :a])
+    assert torch.equal(dec.v_cache[:, :, :a], vp[:, :, :a])
+    kc = dec.k_cache.float().cpu()
+    assert _close_bf16(dec.v_cache[0, :, :n].float().cpu(), orc.v_cache[0, :, :n])
+    assert _close_bf16(kc[0, :, :n], orc.k_cache[0, :, :n], head_ulp=True)
+    dec.reset()
+    tok2, lg = dec.prefill_asr(toks, audio.cuda(), a, return_logits=True)
+    err = float((lg.cpu() - olg).abs().max())
+    print(f"prefill_asr: logit error {err:.3e}")
+    assert tok2 == tok and err <= 4e-2
+    if top2_margin(olg) > 2 * err + 1e-6:
+        assert tok == otok
+    dec.reset()
+    _, glg = dec.prefill_step_with_logits(toks)   # unpatched logits differ from the patched ones
+    assert float((glg.cpu() - olg).abs().max()) > 1e-3
+    for bad_start, emb in ((n - m + 1, audio.cuda()), (-1, audio.cuda()),
+                           (0, audio.cuda()[:0]), (0, audio.float().cuda()), (0, audio)):
+        with pytest.raises(RuntimeError):
+            dec.prefill_asr(toks, emb, bad_start)
+    with pytest.raises(RuntimeError):
+        dec.prefill_asr(torch.zeros(513, dtype=torch.int32), audio.cuda(), 0)
+    dec.check()
+
+
 def test_prefill_errors(small):
     dec, _, sp, _ = small
     with pytest.raises(RuntimeError):

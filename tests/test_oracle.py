@@ -188,6 +188,26 @@ def test_prefill_errors_and_position():
     assert m.position == 0 and float(m.k_cache.abs().sum()) == 0.0
 
 
+def test_prefill_embedding_patch_pins():
+    """The prefill_asr embedding patch (bindings_prefill.cpp:835-955): patching a span with the
+    token embeddings it replaces is the identity; a different span changes the logits but, by
+    causality, leaves every K/V row before the span bit-identical in every layer."""
+    m, spec = _tiny_model()
+    toks = make_tokens(12, spec["vocab_size"], seed=4)
+    _, l0 = m.prefill(toks)
+    k0, v0 = m.k_cache.clone(), m.v_cache.clone()
+    _, l1 = m.prefill(toks, embeds=m.embed[toks[5:9]], embeds_start=5)
+    assert torch.equal(l0, l1) and torch.equal(k0, m.k_cache)
+    audio = bf16(torch.randn(4, m.embed.shape[1], generator=torch.Generator().manual_seed(3)))
+    _, l2 = m.prefill(toks, embeds=audio, embeds_start=5)
+    assert float((l2 - l0).abs().max()) > 1e-3
+    assert torch.equal(k0[:, :, :5], m.k_cache[:, :, :5])
+    assert torch.equal(v0[:, :, :5], m.v_cache[:, :, :5])
+    assert not torch.equal(k0[:, :, 5:12], m.k_cache[:, :, 5:12])
+    with pytest.raises(RuntimeError):
+        m.prefill(toks, embeds=audio, embeds_start=9)
+
+
 def test_synthetic_weights_are_seeded_and_canonical():
     spec = dict(hidden_size=64, intermediate_size=96, num_q_heads=4, num_kv_heads=2, head_dim=16,
                 num_layers=2, vocab_size=50)
