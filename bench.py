@@ -172,6 +172,20 @@ def pmc_workload():
     print(f"pmc workload done: 256 MiB copy, prefill 128, decode 16 -> {toks[-1].item()}")
 
 
+def prefill_workload(n: int):
+    """One n-token prefill (after one warm-up call) for counter runs of the prefill kernels."""
+    import torch
+    from megaqwen_amd.synthetic import make_tokens
+    dec, _ = build_decoder(n + 8, max_prefill=n)
+    toks = make_tokens(n, 151936, seed=1)
+    dec.prefill_step(toks)
+    dec.reset()
+    tok = dec.prefill_step(toks)
+    torch.cuda.synchronize()
+    dec.check()
+    print(f"prefill workload done: 2 x prefill {n} -> {tok}")
+
+
 def cpu_baseline(prompt_len: int = 16, gen: int = 32):
     import torch
     from megaqwen_amd.rope import build_rope_tables
@@ -219,6 +233,8 @@ def main():
                     help="short fixed workload for hardware-counter runs: a 256 MiB device copy "
                          "(calibration of FETCH_SIZE / WRITE_SIZE), a 128-token prefill, then 16 "
                          "decode steps at positions 128..143")
+    ap.add_argument("--prefill-workload", type=int, default=0, metavar="N",
+                    help="for counter runs of the prefill kernels: two N-token prefills, nothing else")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): the decode and prefill "
@@ -228,6 +244,9 @@ def main():
     import torch
     if args.pmc_workload:
         pmc_workload()
+        return
+    if args.prefill_workload > 0:
+        prefill_workload(args.prefill_workload)
         return
     K, W = int(args.steps), int(args.warmup)
     positions = (1, 128, 4096)
