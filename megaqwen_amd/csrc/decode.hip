@@ -89,6 +89,9 @@ struct RowSet {
         const bf16_t* r = rowptr(it / S) + (it % S) * KS + lane * 8;
 #pragma unroll
         for (int l = 0; l < NL; ++l) w[j][l] = ld_nt16(r + l * 512);
+      } else {
+#pragma unroll
+        for (int l = 0; l < NL; ++l) w[j][l] = make_uint4(0, 0, 0, 0);
       }
     }
   }
@@ -98,17 +101,20 @@ struct RowSet {
     const int lane = lane_id(), wave = wave_id();
     if (wave >= MQ_CWAVES) return;
     const int nitems = nr * S;
+    // all PF items as straight-line code (items past nitems hold zero weights), so the x reads
+    // are shared and the four reductions run as one (sum4_rows: item j's total in lanes 16j..)
+    static_assert(PF <= 4, "sum4_rows reduces four items");
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      const int it = wave + j * MQ_CWAVES;
-      if (it < nitems) {
-        const float* xs = x + (it % S) * KS + lane * 8;
-        float acc = 0.f;
+      const float* xs = x + ((wave + j * MQ_CWAVES) % S) * KS + lane * 8;
 #pragma unroll
-        for (int l = 0; l < NL; ++l) acc = dot8_lds(w[j][l], xs + l * 512, acc);
-        acc = wave_sum(acc);
-        if (lane == 0) out(it, acc);
-      }
+      for (int l = 0; l < NL; ++l) acc[j] = dot8_lds(w[j][l], xs + l * 512, acc[j]);
+    }
+    {
+      const float tot = sum4_rows(acc[0], acc[1], acc[2], acc[3]);
+      const int j = lane >> 4, it = wave + j * MQ_CWAVES;
+      if ((lane & 15) == 0 && j < PF && it < nitems) out(it, tot);
     }
     for (int it = wave + PF * MQ_CWAVES; it < nitems; it += MQ_CWAVES) {
       const bf16_t* r = rowptr(it / S) + (it % S) * KS + lane * 8;
@@ -874,13 +880,17 @@ struct PairSet {
     if (wave >= MQ_CWAVES) return;
     const int np = (nr + 1) / 2;
     const float* xs = x + (lane & 31) * 8;
+    // items i and i + 1 are reduced together by sum2_halves: lane group k = lane / 16 receives
+    // the total of item i + (k & 1), row 2 it + (k >> 1) (the low / high 32-lane half); items past
+    // np hold zero weights
 #pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int it = wave + i * MQ_CWAVES, row = 2 * it + (lane >> 5);
-      if (it < np) {
-        const float acc = sum_xor16(row16_sum(dot8_lds(w[i], xs, 0.f)));
-        if ((lane & 31) == 0 && row < nr) out(row, acc);
-      }
+    for (int i = 0; i < PF; i += 2) {
+      const float a0 = dot8_lds(w[i], xs, 0.f);
+      const float a1 = i + 1 < PF ? dot8_lds(w[i + 1 < PF ? i + 1 : i], xs, 0.f) : 0.f;
+      const float tot = sum2_halves(a0, a1);
+      const int k = lane >> 4, ii = i + (k & 1);
+      const int it = wave + ii * MQ_CWAVES, row = 2 * it + (k >> 1);
+      if ((lane & 15) == 0 && ii < PF && it < np && row < nr) out(row, tot);
     }
     for (int it = wave + PF * MQ_CWAVES; it < np; it += MQ_CWAVES) {
       const int row = 2 * it + (lane >> 5);

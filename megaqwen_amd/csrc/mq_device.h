@@ -117,6 +117,30 @@ MQ_DEV float2 swap32(float v) {
                                                   false);
   return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// Totals of four per-lane partial sums a0..a3 over the 64 lanes, with two row exchanges per
+// step instead of one per value: v_permlane32_swap(a, b) yields (a_lo | b_lo, a_hi | b_hi), so
+// one swap + add folds a over lanes ^32 into lanes 0-31 and b into lanes 32-63; then
+// v_permlane16_swap of the two folds leaves value j folded over lanes ^16 and ^32 in lanes
+// 16j..16j+15, and a DPP row sum finishes it.  Lanes 16j..16j+15 receive the total of aj.
+MQ_DEV float sum4_rows(float a0, float a1, float a2, float a3) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a0), __float_as_uint(a2), false,
+                                                  false);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(a1), __float_as_uint(a3), false,
+                                                  false);
+  const float x0 = __uint_as_float(p[0]) + __uint_as_float(p[1]);   // a0 | a2
+  const float x1 = __uint_as_float(q[0]) + __uint_as_float(q[1]);   // a1 | a3
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x0), __float_as_uint(x1), false,
+                                                  false);
+  return row16_sum(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+}
+// Totals over 32-lane halves of two values (a0: lanes 0-31 | lanes 32-63 are two sums, same for
+// a1): lanes 0-15 receive a0's low-half total, 16-31 a1's low-half total, 32-47 a0's high-half
+// total, 48-63 a1's high-half total.
+MQ_DEV float sum2_halves(float a0, float a1) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a0), __float_as_uint(a1), false,
+                                                  false);
+  return row16_sum(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+}
 MQ_DEV float sum_xor16(float v) { const float2 p = swap16(v); return p.x + p.y; }
 MQ_DEV float sum_xor32(float v) { const float2 p = swap32(v); return p.x + p.y; }
 MQ_DEV float max_xor16(float v) { const float2 p = swap16(v); return fmaxf(p.x, p.y); }
