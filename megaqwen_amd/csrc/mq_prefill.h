@@ -10,8 +10,9 @@ struct MqPrefillBuffers {
   bf16_t* qkv;   // [n, 4096] q | k | v projections (q/k rotated in place)
   bf16_t* att;   // [n, 2048] attention output
   bf16_t* m;     // [n, 3072] silu(gate) * up
-  bf16_t* vt;    // [8 * 128, ldvt] V transposed (dims x positions) for the causal attention
-  int ldvt;      // max_n rounded up to 32
+  bf16_t* vt;    // V^T of each kv head in attention-operand tile order (prefill.hip vt_index)
+  bf16_t* kt;    // K of each kv head in attention-operand tile order (prefill.hip kt_index)
+  int ntiles;    // 32-key tiles per kv head in vt / kt (max_n rounded up)
 };
 
 size_t mq_prefill_workspace_bytes(int max_n);

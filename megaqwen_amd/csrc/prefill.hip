@@ -33,6 +33,27 @@ MQ_DEV uint32_t pack_bf16x2(float a, float b) {
   return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
 }
 
+// ------------------------------------------------------------ attention operand layouts
+// The causal attention reads K and V^T as MFMA operands, 16 bytes per lane.  Both are kept, per
+// kv head and 32-key tile, in the exact order the operand registers take them, so every operand
+// load of the attention is one contiguous 1 KB wave load (the KV cache rows stay [pos][128] for
+// decode; these are prefill-only copies).
+//   K  (A operand of S^T = K Q^T):   [h][tile][s 0..7][lane][8];  lane = row + 32 hh holds key
+//       32 tile + att_key_perm(row), dims 16 s + 8 hh .. + 8
+//   V^T (A operand of O^T += V^T P^T): [h][tile][nt 0..3][s 0..1][lane][8];  lane = c + 32 hh
+//       holds dim 32 nt + c, keys 32 tile + 16 s + 8 hh .. + 8
+// att_key_perm swaps bits 2 and 3 of a tile row (an involution); the reason is given at the
+// attention kernel.
+MQ_DEV int att_key_perm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+MQ_DEV size_t kt_index(int h, int ntiles, int key, int d) {
+  const int t = key >> 5, row = att_key_perm(key & 31), s = d >> 4, hh = (d >> 3) & 1;
+  return ((((size_t)h * ntiles + t) * 8 + s) * 64 + row + 32 * hh) * 8 + (d & 7);
+}
+MQ_DEV size_t vt_index(int h, int ntiles, int key, int d) {
+  const int t = key >> 5, kk = key & 31, s = kk >> 4, hh = (kk >> 3) & 1, nt = d >> 5;
+  return (((((size_t)h * ntiles + t) * 4 + nt) * 2 + s) * 64 + (d & 31) + 32 * hh) * 8 + (kk & 7);
+}
+
 // ------------------------------------------------------------------------- row kernels
 // Embedding gather (prefill_embed_kernel, fused_prefill_kernels.inl:3-20); rows
 // [patch_start, patch_start + patch_len) take the caller's bf16 rows instead (the audio span of
@@ -78,35 +99,66 @@ __global__ void __launch_bounds__(128) pf_rmsnorm_kernel(const bf16_t* __restric
 }
 
 // Per-(position, head) q/k RMSNorm + rotate-half RoPE, rounded to bf16 in place; k and v rows go
-// to the KV cache of `layer` (prefill_qk_norm_rope_kernel, fused_prefill_kernels.inl:112-258).
-// One wave per (position, head); heads 0..15 are q, 16..23 are k (with v).
+// to the KV cache of `layer` and k also to the attention's operand copy
+// (prefill_qk_norm_rope_kernel, fused_prefill_kernels.inl:112-258).  One wave per position and 4
+// heads of the 24 (0..15 q, 16..23 k with v): lane group g = lane / 16 takes head 4 blockIdx.y + g,
+// lane i = lane % 16 dims 4i .. 4i + 3 and their RoPE partners 64 + 4i .. 64 + 4i + 3 (8-byte
+// accesses).
 __global__ void __launch_bounds__(64) pf_qk_norm_rope_kernel(MqDecodeParams p, int layer,
-                                                             bf16_t* __restrict__ qkv) {
-  const int pos = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+                                                             bf16_t* __restrict__ qkv,
+                                                             bf16_t* __restrict__ kt, int ntiles) {
+  const int pos = blockIdx.x, lane = threadIdx.x, i = lane & 15;
+  const int head = 4 * blockIdx.y + (lane >> 4);
   const MqLayerW w = p.layers[layer];
-  const bf16_t* cs = p.cos + (size_t)pos * MQ_D;
-  const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
   bf16_t* row = qkv + (size_t)pos * MQ_QKV;
   const bool is_q = head < MQ_NQ;
   const int h = is_q ? head : head - MQ_NQ;
   bf16_t* x = row + (is_q ? h * MQ_D : MQ_QDIM + h * MQ_D);
-  float lo = bf16_to_f32(x[lane]), hi = bf16_to_f32(x[lane + 64]);
-  const bf16_t* nw = is_q ? w.q_norm : w.k_norm;
-  const float ss = wave_sum(lo * lo + hi * hi);
+  const int d0 = 4 * i;
+  const uint2 xl = *reinterpret_cast<const uint2*>(x + d0);
+  const uint2 xh = *reinterpret_cast<const uint2*>(x + 64 + d0);
+  const float lo[4] = {bf16_lo(xl.x), bf16_hi(xl.x), bf16_lo(xl.y), bf16_hi(xl.y)};
+  const float hi[4] = {bf16_lo(xh.x), bf16_hi(xh.x), bf16_lo(xh.y), bf16_hi(xh.y)};
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
+  ss = row16_sum(ss);
   const float r = rsqrtf(ss * (1.0f / MQ_D) + MQ_EPS);
-  const float a = lo * r * bf16_to_f32(nw[lane]);
-  const float b = hi * r * bf16_to_f32(nw[lane + 64]);
-  const bf16_t olo = f32_to_bf16(a * bf16_to_f32(cs[lane]) - b * bf16_to_f32(sn[lane]));
-  const bf16_t ohi = f32_to_bf16(a * bf16_to_f32(sn[lane + 64]) + b * bf16_to_f32(cs[lane + 64]));
-  x[lane] = olo;
-  x[lane + 64] = ohi;
+  const bf16_t* nw = is_q ? w.q_norm : w.k_norm;
+  const uint2 nl = *reinterpret_cast<const uint2*>(nw + d0);
+  const uint2 nh = *reinterpret_cast<const uint2*>(nw + 64 + d0);
+  const uint2 cl = *reinterpret_cast<const uint2*>(p.cos + (size_t)pos * MQ_D + d0);
+  const uint2 ch = *reinterpret_cast<const uint2*>(p.cos + (size_t)pos * MQ_D + 64 + d0);
+  const uint2 sl = *reinterpret_cast<const uint2*>(p.sin + (size_t)pos * MQ_D + d0);
+  const uint2 sh = *reinterpret_cast<const uint2*>(p.sin + (size_t)pos * MQ_D + 64 + d0);
+  const float nwl[4] = {bf16_lo(nl.x), bf16_hi(nl.x), bf16_lo(nl.y), bf16_hi(nl.y)};
+  const float nwh[4] = {bf16_lo(nh.x), bf16_hi(nh.x), bf16_lo(nh.y), bf16_hi(nh.y)};
+  const float cosl[4] = {bf16_lo(cl.x), bf16_hi(cl.x), bf16_lo(cl.y), bf16_hi(cl.y)};
+  const float cosh_[4] = {bf16_lo(ch.x), bf16_hi(ch.x), bf16_lo(ch.y), bf16_hi(ch.y)};
+  const float sinl[4] = {bf16_lo(sl.x), bf16_hi(sl.x), bf16_lo(sl.y), bf16_hi(sl.y)};
+  const float sinh_[4] = {bf16_lo(sh.x), bf16_hi(sh.x), bf16_lo(sh.y), bf16_hi(sh.y)};
+  bf16_t olo[4], ohi[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = lo[e] * r * nwl[e], b = hi[e] * r * nwh[e];
+    olo[e] = f32_to_bf16(a * cosl[e] - b * sinl[e]);
+    ohi[e] = f32_to_bf16(a * sinh_[e] + b * cosh_[e]);
+  }
+  const uint2 ol = make_uint2((uint32_t)olo[0] | ((uint32_t)olo[1] << 16),
+                              (uint32_t)olo[2] | ((uint32_t)olo[3] << 16));
+  const uint2 oh = make_uint2((uint32_t)ohi[0] | ((uint32_t)ohi[1] << 16),
+                              (uint32_t)ohi[2] | ((uint32_t)ohi[3] << 16));
+  *reinterpret_cast<uint2*>(x + d0) = ol;
+  *reinterpret_cast<uint2*>(x + 64 + d0) = oh;
   if (!is_q) {
     const size_t crow = (((size_t)layer * MQ_NKV + h) * p.max_seq + pos) * MQ_D;
-    p.kc[crow + lane] = olo;
-    p.kc[crow + lane + 64] = ohi;
+    *reinterpret_cast<uint2*>(p.kc + crow + d0) = ol;
+    *reinterpret_cast<uint2*>(p.kc + crow + 64 + d0) = oh;
+    *reinterpret_cast<uint2*>(kt + kt_index(h, ntiles, pos, d0)) = ol;
+    *reinterpret_cast<uint2*>(kt + kt_index(h, ntiles, pos, 64 + d0)) = oh;
     const bf16_t* v = row + MQ_QDIM + MQ_KVDIM + h * MQ_D;
-    p.vc[crow + lane] = v[lane];
-    p.vc[crow + lane + 64] = v[lane + 64];
+    *reinterpret_cast<uint2*>(p.vc + crow + d0) = *reinterpret_cast<const uint2*>(v + d0);
+    *reinterpret_cast<uint2*>(p.vc + crow + 64 + d0) = *reinterpret_cast<const uint2*>(v + 64 + d0);
   }
 }
 
@@ -125,8 +177,8 @@ struct GemmArgs {
   int ldc;
   const bf16_t* R;   // EPI_RESID: residual [M, N] (may alias C)
   int ldr;
-  bf16_t* Vt;        // EPI_STORE: columns [n1, N) also stored transposed, Vt[(col - n1) * ldvt + row]
-  int ldvt;
+  bf16_t* Vt;        // EPI_STORE: columns [n1, N) (V) also stored as V^T operand tiles (vt_index)
+  int vt_tiles;      // 32-row tiles per kv head in Vt
   int M, N, K;
 };
 
@@ -276,20 +328,22 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
     }
   }
   if (EPI == EPI_STORE && g.Vt != nullptr && n_base >= g.n1) {
-    // V^T for the prefill attention: accumulator elements 4 jg .. 4 jg + 3 are 4 consecutive rows
-    bf16_t* vt = g.Vt + (size_t)(col - g.n1) * g.ldvt;
+    // V^T operand tiles: accumulator elements 4 jg .. 4 jg + 3 are 4 consecutive keys (rows),
+    // which are 4 consecutive bf16 of one V^T lane slot
+    const int d = col - g.n1, h = d >> 7, dd = d & 127;
 #pragma unroll
     for (int jg = 0; jg < 4; ++jg) {
       const int row = m_base + wm * 32 + 8 * jg + 4 * (lane >> 5);
+      bf16_t* dst = g.Vt + vt_index(h, g.vt_tiles, row, dd);
       if (row + 3 < g.M) {
         uint2 w;
         w.x = pack_bf16x2(acc[0][4 * jg], acc[0][4 * jg + 1]);
         w.y = pack_bf16x2(acc[0][4 * jg + 2], acc[0][4 * jg + 3]);
-        *reinterpret_cast<uint2*>(vt + row) = w;
+        *reinterpret_cast<uint2*>(dst) = w;
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (row + e < g.M) vt[row + e] = f32_to_bf16(acc[0][4 * jg + e]);
+          if (row + e < g.M) dst[e] = f32_to_bf16(acc[0][4 * jg + e]);
       }
     }
   }
@@ -311,7 +365,6 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
 // close to the reference's fp32 weights.  V^T (dims x keys) is written by the QKV GEMM epilogue.
 #define ATT_KT 32
 
-MQ_DEV int att_key_perm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
 // A workgroup is one (query head, 32-query block); its blockDim.x / 64 waves (<= ATT_SPLIT) split
 // the block's key tiles into contiguous ranges and merge their (max, sum, O) partials through LDS
@@ -325,7 +378,8 @@ MQ_DEV int att_key_perm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >>
 
 __global__ void __launch_bounds__(64 * ATT_SPLIT) __attribute__((amdgpu_waves_per_eu(2)))
 pf_attn_kernel(MqDecodeParams p, int layer, const bf16_t* __restrict__ qkv,
-               const bf16_t* __restrict__ vt, int ldvt, bf16_t* __restrict__ att, int n) {
+               const bf16_t* __restrict__ kop, const bf16_t* __restrict__ vop, int ntiles,
+               bf16_t* __restrict__ att, int n) {
   __shared__ float red[ATT_SPLIT - 1][66][64];     // waves 1.. : o (64 per lane), m, l
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   // kv head h = blockIdx.x % 8 is the XCD the workgroup runs on (workgroups are dealt to the 8
@@ -336,8 +390,9 @@ pf_attn_kernel(MqDecodeParams p, int layer, const bf16_t* __restrict__ qkv,
   const int fr = lane & 31, hh = lane >> 5;
   const int q = q0 + fr;                           // this lane's query position
   const int t0 = (qb + 1) * wave / nw, t1 = (qb + 1) * (wave + 1) / nw;   // key tiles of this wave
-  const bf16_t* Kc = p.kc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
-  const bf16_t* Vt = vt + (size_t)h * MQ_D * ldvt;
+  // this kv head's operand tiles (see kt_index / vt_index): tile t starts at 4096 * t
+  const bf16_t* Kt = kop + (size_t)h * ntiles * 4096 + lane * 8;
+  const bf16_t* Vt = vop + (size_t)h * ntiles * 4096 + lane * 8;
 
   // Q^T operand: query q, dims 16 s + 8 hh .. + 8 (rows past n read row n - 1, never stored)
   mq_bf16x8 qf[8];
@@ -346,14 +401,12 @@ pf_attn_kernel(MqDecodeParams p, int layer, const bf16_t* __restrict__ qkv,
 #pragma unroll
     for (int s = 0; s < 8; ++s) qf[s] = as_bf16x8(ld16(src + 16 * s));
   }
-  // K operand: key att_key_perm(fr) of the tile, dims 16 s + 8 hh .. + 8
-  const bf16_t* ksrc = Kc + (size_t)att_key_perm(fr) * MQ_D + 8 * hh;
-  const int kmax = n - 1 - att_key_perm(fr);       // keys past n - 1 read row n - 1
+  // K operand of tile t: key 32 t + att_key_perm(fr), dims 16 s + 8 hh .. + 8 (slots of keys
+  // >= n hold stale values; their scores are masked)
   uint4 kf[8];
-  auto load_k = [&](int kt) {
-    const bf16_t* src = ksrc + (size_t)min(kt * ATT_KT, kmax) * MQ_D;
+  auto load_k = [&](int t) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) kf[s] = ld16(src + 16 * s);
+    for (int s = 0; s < 8; ++s) kf[s] = ld16(Kt + (size_t)t * 4096 + s * 512);
   };
 
   mq_f32x16 o[4];
@@ -373,8 +426,7 @@ pf_attn_kernel(MqDecodeParams p, int layer, const bf16_t* __restrict__ qkv,
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
-        vf[nt][s] = ld16(Vt + (size_t)(32 * nt + fr) * ldvt + k0 + 16 * s + 8 * hh);
+      for (int s = 0; s < 2; ++s) vf[nt][s] = ld16(Vt + (size_t)kt * 4096 + (2 * nt + s) * 512);
     mq_f32x16 sacc;
 #pragma unroll
     for (int j = 0; j < 16; ++j) sacc[j] = 0.f;
@@ -502,21 +554,22 @@ pf_attn_kernel(MqDecodeParams p, int layer, const bf16_t* __restrict__ qkv,
 // -------------------------------------------------------------------------- host side
 static size_t pf_align(size_t v) { return (v + 255) / 256 * 256; }
 
-// V^T rows hold whole 32-key tiles
-static int pf_ldvt(int max_n) { return (max_n + 31) / 32 * 32; }
+// 32-key tiles per kv head of the K / V^T operand copies
+static int pf_tiles(int max_n) { return (max_n + 31) / 32; }
 
 size_t mq_prefill_workspace_bytes(int max_n) {
   if (max_n <= 0) return 0;
   const size_t n = (size_t)max_n;
   return pf_align(n * MQ_H * 2) * 2 + pf_align(n * MQ_QKV * 2) + pf_align(n * MQ_QDIM * 2) +
-         pf_align(n * MQ_I * 2) + pf_align((size_t)MQ_KVDIM * pf_ldvt(max_n) * 2);
+         pf_align(n * MQ_I * 2) + 2 * pf_align((size_t)MQ_NKV * pf_tiles(max_n) * 4096 * 2);
 }
 
 void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n) {
   b->max_n = max_n;
   if (max_n <= 0) {
     b->h = b->xn = b->qkv = b->att = b->m = b->vt = nullptr;
-    b->ldvt = 0;
+    b->kt = nullptr;
+    b->ntiles = 0;
     return;
   }
   const size_t n = (size_t)max_n;
@@ -527,7 +580,9 @@ void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n) {
   b->att = reinterpret_cast<bf16_t*>(c); c += pf_align(n * MQ_QDIM * 2);
   b->m = reinterpret_cast<bf16_t*>(c);    c += pf_align(n * MQ_I * 2);
   b->vt = reinterpret_cast<bf16_t*>(c);
-  b->ldvt = pf_ldvt(max_n);
+  b->ntiles = pf_tiles(max_n);
+  c += pf_align((size_t)MQ_NKV * b->ntiles * 4096 * 2);
+  b->kt = reinterpret_cast<bf16_t*>(c);
 }
 
 // K must be a multiple of 256 and N of 64 (every Qwen3-0.6B projection is).  Tiles of 32 rows
@@ -559,11 +614,12 @@ int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefi
     g.A = b.xn; g.lda = MQ_H;
     g.B0 = w.wq; g.B1 = w.wk; g.B2 = w.wv; g.n0 = MQ_QDIM; g.n1 = MQ_QDIM + MQ_KVDIM;
     g.C = b.qkv; g.ldc = MQ_QKV; g.M = n; g.N = MQ_QKV; g.K = MQ_H;
-    g.Vt = b.vt; g.ldvt = b.ldvt;
+    g.Vt = b.vt; g.vt_tiles = b.ntiles;
     gemm<EPI_STORE>(g, stream);
-    pf_qk_norm_rope_kernel<<<dim3(n, MQ_NQ + MQ_NKV), 64, 0, stream>>>(p, l, b.qkv);
+    pf_qk_norm_rope_kernel<<<dim3(n, (MQ_NQ + MQ_NKV) / 4), 64, 0, stream>>>(p, l, b.qkv, b.kt,
+                                                                            b.ntiles);
     pf_attn_kernel<<<dim3(MQ_NQ, (n + 31) / 32), 64 * ATT_SPLIT, 0, stream>>>(
-        p, l, b.qkv, b.vt, b.ldvt, b.att, n);
+        p, l, b.qkv, b.kt, b.vt, b.ntiles, b.att, n);
     g = GemmArgs{};
     g.A = b.att; g.lda = MQ_QDIM;
     g.B0 = g.B1 = g.B2 = w.wo; g.n0 = g.n1 = MQ_H;
