@@ -182,33 +182,40 @@ struct GemmArgs {
   int M, N, K;
 };
 
-#define GEMM_BN 64
 #define GEMM_BK 64
 #define GEMM_LDS_STRIDE 72   // bf16 per LDS row: 64 + 8 padding (16-byte chunk c of row r at 9r + c)
-#define GEMM_STAGES 4        // K steps whose global loads are in flight in registers
+#define GEMM_STAGES 4        // K steps whose global loads are in flight in registers (64-row tiles)
+#define GEMM_STAGES_BIG 2    // the same for 128-row tiles, so two of their waves fit on a SIMD
 
-// One BM x 64 tile of C per workgroup of 4 waves, K in steps of 64.  The global loads of step
-// k + GEMM_STAGES are issued while step k is multiplied: a ring of GEMM_STAGES register slots
-// feeds a double-buffered LDS tile, so about 4 x 16 KB per workgroup are in flight.
-//   BM = 64: waves form a 2 x 2 grid of 32 x 32 blocks.
-//   BM = 32: waves 0/1 and 2/3 compute the same two 32 x 32 blocks over the first and the
-//            second half of every K step; the halves are added in LDS before the epilogue
+// One BM x BN tile of C per workgroup of 4 waves, K in steps of 64.  The global loads of step
+// k + S are issued while step k is multiplied: a ring of S register slots (GEMM_STAGES, or
+// GEMM_STAGES_BIG for 128-row tiles) feeds a double-buffered LDS tile.
+//   BM = 64 / 128: waves form a 2 x 2 grid of (BM / 2) x (BN / 2) tiles, each made of 32 x 32
+//            MFMA blocks (128 x 128 tiles halve the L2 traffic per flop of 64 x 64 ones and are
+//            used when there are enough of them to fill the CUs).
+//   BM = 32 (BN = 64): waves 0/1 and 2/3 compute the same two 32 x 32 blocks over the first and
+//            the second half of every K step; the halves are added in LDS before the epilogue
 //            (this doubles the workgroups of the N = 1024 GEMMs at M = 512).
-template <int EPI, int BM>
+template <int EPI, int BM, int BN>
 __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
   constexpr int NB = EPI == EPI_SWIGLU ? 2 : 1;   // weight tiles per step (gate and up)
   constexpr int KG = BM == 32 ? 2 : 1;            // wave groups splitting each K step
+  constexpr int WM = KG == 2 ? 32 : BM / 2;       // rows of a wave's tile
+  constexpr int WN = BN / 2;                      // columns of a wave's tile
+  constexpr int MB = WM / 32, NBK = WN / 32;      // 32 x 32 MFMA blocks per wave tile
   constexpr int NA = BM / 32;                     // 16-byte A loads per thread per step
-  constexpr int NL = GEMM_BN / 32;                // 16-byte loads per weight tile per thread
-  constexpr int S = GEMM_STAGES;
-  static_assert(BM == 32 || BM == 64, "tile rows");
+  constexpr int NL = BN / 32;                     // 16-byte loads per weight tile per thread
+  constexpr int S = BM == 128 ? GEMM_STAGES_BIG : GEMM_STAGES;
+  static_assert(BM == 32 || BM == 64 || BM == 128, "tile rows");
+  static_assert(BN == 64 || BN == 128, "tile columns");
+  static_assert(KG == 1 || BN == 64, "the K-split layout covers 32 x 64 tiles");
   __shared__ __align__(16) bf16_t As[2][BM * GEMM_LDS_STRIDE];
-  __shared__ __align__(16) bf16_t Bs[2][NB][GEMM_BN * GEMM_LDS_STRIDE];
+  __shared__ __align__(16) bf16_t Bs[2][NB][BN * GEMM_LDS_STRIDE];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wn = wave & 1;
   const int wm = KG == 1 ? (wave >> 1) : 0;
   const int wk = KG == 2 ? (wave >> 1) : 0;
-  const int n_base = blockIdx.x * GEMM_BN, m_base = blockIdx.y * BM;
+  const int n_base = blockIdx.x * BN, m_base = blockIdx.y * BM;
   const bf16_t* B;
   if (n_base < g.n0) B = g.B0 + (size_t)n_base * g.K;
   else if (n_base < g.n1) B = g.B1 + (size_t)(n_base - g.n0) * g.K;
@@ -249,25 +256,37 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
         *reinterpret_cast<uint4*>(&Bs[buf][j][(sr + 32 * i) * GEMM_LDS_STRIDE + sk]) = b[j][i];
   };
 
-  mq_f32x16 acc[NB];
+  mq_f32x16 acc[NB][MB][NBK];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[b][j] = 0.f;
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[b][mb][nb][j] = 0.f;
 
   const int fr = lane & 31, fk = (lane >> 5) * 8;   // MFMA operand row and k offset of a lane
   auto mma_step = [&](int buf) {
 #pragma unroll
     for (int q = 0; q < 4 / KG; ++q) {
       const int kofs = 16 * (q + wk * (4 / KG)) + fk;
-      const mq_bf16x8 af = as_bf16x8(
-          *reinterpret_cast<const uint4*>(&As[buf][(wm * 32 + fr) * GEMM_LDS_STRIDE + kofs]));
+      mq_bf16x8 af[MB];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const mq_bf16x8 bf = as_bf16x8(*reinterpret_cast<const uint4*>(
-            &Bs[buf][b][(wn * 32 + fr) * GEMM_LDS_STRIDE + kofs]));
-        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc[b], 0, 0, 0);
-      }
+      for (int mb = 0; mb < MB; ++mb)
+        af[mb] = as_bf16x8(*reinterpret_cast<const uint4*>(
+            &As[buf][(wm * WM + mb * 32 + fr) * GEMM_LDS_STRIDE + kofs]));
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int nb = 0; nb < NBK; ++nb) {
+          const mq_bf16x8 bf = as_bf16x8(*reinterpret_cast<const uint4*>(
+              &Bs[buf][b][(wn * WN + nb * 32 + fr) * GEMM_LDS_STRIDE + kofs]));
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            acc[b][mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], bf, acc[b][mb][nb],
+                                                                     0, 0, 0);
+        }
     }
   };
 
@@ -301,53 +320,61 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
     float* red = reinterpret_cast<float*>(&As[0][0]);
     if (wk == 1) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) red[(wn * 16 + j) * 64 + lane] = acc[0][j];
+      for (int j = 0; j < 16; ++j) red[(wn * 16 + j) * 64 + lane] = acc[0][0][0][j];
     }
     __syncthreads();
     if (wk == 1) return;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[0][j] += red[(wn * 16 + j) * 64 + lane];
+    for (int j = 0; j < 16; ++j) acc[0][0][0][j] += red[(wn * 16 + j) * 64 + lane];
   }
 
-  // epilogue: acc[j] is C[row][col] with row = 8*(j/4) + 4*(lane/32) + j%4, col = lane%32
-  const int col = n_base + wn * 32 + (lane & 31);
+  // epilogue: acc[.][mb][nb][j] is C[row][col] with row = 32 mb + 8 (j / 4) + 4 (lane / 32) +
+  // j % 4, col = 32 nb + lane % 32 within the wave's tile
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int row = m_base + wm * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-    if (row < g.M) {
-      float v;
-      if (EPI == EPI_STORE) {
-        v = acc[0][j];
-      } else if (EPI == EPI_RESID) {
-        v = round_bf16(acc[0][j]) + bf16_to_f32(g.R[(size_t)row * g.ldr + col]);
-      } else {
-        const float gv = round_bf16(acc[0][j]), uv = round_bf16(acc[NB - 1][j]);
-        v = silu_f(gv) * uv;
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NBK; ++nb) {
+      const int col = n_base + wn * WN + nb * 32 + (lane & 31);
+      const int rbase = m_base + wm * WM + mb * 32;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int row = rbase + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        if (row < g.M) {
+          float v;
+          if (EPI == EPI_STORE) {
+            v = acc[0][mb][nb][j];
+          } else if (EPI == EPI_RESID) {
+            v = round_bf16(acc[0][mb][nb][j]) + bf16_to_f32(g.R[(size_t)row * g.ldr + col]);
+          } else {
+            const float gv = round_bf16(acc[0][mb][nb][j]), uv = round_bf16(acc[NB - 1][mb][nb][j]);
+            v = silu_f(gv) * uv;
+          }
+          g.C[(size_t)row * g.ldc + col] = f32_to_bf16(v);
+        }
       }
-      g.C[(size_t)row * g.ldc + col] = f32_to_bf16(v);
-    }
-  }
-  if (EPI == EPI_STORE && g.Vt != nullptr && n_base >= g.n1) {
-    // V^T operand tiles: accumulator elements 4 jg .. 4 jg + 3 are 4 consecutive keys (rows),
-    // which are 4 consecutive bf16 of one V^T lane slot
-    const int d = col - g.n1, h = d >> 7, dd = d & 127;
+      if (EPI == EPI_STORE && g.Vt != nullptr && n_base >= g.n1) {
+        // V^T operand tiles: accumulator elements 4 jg .. 4 jg + 3 are 4 consecutive keys (rows),
+        // which are 4 consecutive bf16 of one V^T lane slot
+        const int d = col - g.n1, h = d >> 7, dd = d & 127;
 #pragma unroll
-    for (int jg = 0; jg < 4; ++jg) {
-      const int row = m_base + wm * 32 + 8 * jg + 4 * (lane >> 5);
-      bf16_t* dst = g.Vt + vt_index(h, g.vt_tiles, row, dd);
-      if (row + 3 < g.M) {
-        uint2 w;
-        w.x = pack_bf16x2(acc[0][4 * jg], acc[0][4 * jg + 1]);
-        w.y = pack_bf16x2(acc[0][4 * jg + 2], acc[0][4 * jg + 3]);
-        *reinterpret_cast<uint2*>(dst) = w;
-      } else {
+        for (int jg = 0; jg < 4; ++jg) {
+          const int row = rbase + 8 * jg + 4 * (lane >> 5);
+          bf16_t* dst = g.Vt + vt_index(h, g.vt_tiles, row, dd);
+          if (row + 3 < g.M) {
+            uint2 w;
+            w.x = pack_bf16x2(acc[0][mb][nb][4 * jg], acc[0][mb][nb][4 * jg + 1]);
+            w.y = pack_bf16x2(acc[0][mb][nb][4 * jg + 2], acc[0][mb][nb][4 * jg + 3]);
+            *reinterpret_cast<uint2*>(dst) = w;
+          } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (row + e < g.M) dst[e] = f32_to_bf16(acc[0][4 * jg + e]);
+            for (int e = 0; e < 4; ++e)
+              if (row + e < g.M) dst[e] = f32_to_bf16(acc[0][mb][nb][4 * jg + e]);
+          }
+        }
       }
     }
-  }
 }
+
 
 // --------------------------------------------------------------------- causal attention
 // Flash-style causal GQA attention (prefill_causal_attention_kernel,
@@ -585,18 +612,29 @@ void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n) {
   b->kt = reinterpret_cast<bf16_t*>(c);
 }
 
-// K must be a multiple of 256 and N of 64 (every Qwen3-0.6B projection is).  Tiles of 32 rows
-// are used when 64-row tiles would leave CUs idle (the N = 1024 GEMMs at M <= 1024).
+// K must be a multiple of 256 and N of 128 (every Qwen3-0.6B projection is).  Tile choice:
+// 128 x 128 (128 x 64 for the two SwiGLU matrices) when that still gives >= 512 workgroups
+// (two per CU; large M); otherwise 64 x 64, or 32 x 64 when even 64-row tiles would leave CUs
+// idle (the N = 1024 GEMMs at M <= 1024).
 template <int EPI>
 static void gemm(const GemmArgs& g, hipStream_t s) {
-  const int nt = g.N / GEMM_BN;
-  if constexpr (EPI != EPI_SWIGLU) {
-    if (nt * ((g.M + 63) / 64) < 256) {
-      pf_gemm_kernel<EPI, 32><<<dim3(nt, (g.M + 31) / 32), 256, 0, s>>>(g);
+  const int mt128 = (g.M + 127) / 128;
+  if constexpr (EPI == EPI_SWIGLU) {
+    if ((g.N / 64) * mt128 >= 512) {
+      pf_gemm_kernel<EPI, 128, 64><<<dim3(g.N / 64, mt128), 256, 0, s>>>(g);
+      return;
+    }
+  } else {
+    if ((g.N / 128) * mt128 >= 512) {
+      pf_gemm_kernel<EPI, 128, 128><<<dim3(g.N / 128, mt128), 256, 0, s>>>(g);
+      return;
+    }
+    if ((g.N / 64) * ((g.M + 63) / 64) < 256) {
+      pf_gemm_kernel<EPI, 32, 64><<<dim3(g.N / 64, (g.M + 31) / 32), 256, 0, s>>>(g);
       return;
     }
   }
-  pf_gemm_kernel<EPI, 64><<<dim3(nt, (g.M + 63) / 64), 256, 0, s>>>(g);
+  pf_gemm_kernel<EPI, 64, 64><<<dim3(g.N / 64, (g.M + 63) / 64), 256, 0, s>>>(g);
 }
 
 int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefillBuffers& b,
