@@ -4,11 +4,12 @@
 
 Workload: Qwen3-0.6B architecture (28 layers, hidden 1024, 16/8 heads x 128, MLP 3072, vocab
 151936, tied LM head), seeded N(0, 0.02) bf16 weights (megaqwen_amd.synthetic, seed 0), batch 1,
-greedy decode.  A step is one decoded token (one persistent decode kernel launch).  Exactly K
-steps are timed at each position bucket: positions 1..K, 128..127+K (the headline `value`) and
-4096..4095+K; each bucket starts from an untimed prefill of that many uniform-random tokens
-(seed 1), as BASELINE config 5 does for 4096.  Inputs are resident in HBM; the timed region is a
-device-side token chain (no host round trip per token).
+greedy decode.  A step is one decoded token.  Exactly K steps are timed at each position bucket:
+positions 1..K, 128..127+K (the headline `value`) and 4096..4095+K; each bucket starts from an
+untimed prefill of that many uniform-random tokens (seed 1), as BASELINE config 5 does for 4096.
+Inputs are resident in HBM; the timed region is a device-side token chain (`mq_decode_steps`: the
+persistent kernel decodes up to 64 chained tokens per launch, no host round trip per token).  The
+rate with one launch per token is reported too (`tok_s_one_launch_per_token`, pos 128).
 
 Prefill: a 512-token uniform-random prompt (seed 1) through the MFMA prefill,
 reported as tokens/s and MFMA utilisation = 481.4 GFLOP (linear 450.97 + causal attention 30.12 +
@@ -16,11 +17,12 @@ last-token LM head 0.31) / time / 2.5 PFLOP/s dense bf16; the 4096-token prefill
 reported too.
 
 Roofline: algorithmic bytes per token = bf16 weights streamed (1,192,101,888 B) + KV read
-(114,688 B x (pos + 1)) + KV write (114,688 B), over the per-launch duration measured with HIP
-events on the launch stream, against 8 TB/s.  `traffic` is the HBM bytes per launch measured by
-two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE over `--pmc-workload`, scaled by what the
-same counters read for a 256 MiB copy), taken from the committed profile summary and reported
-only while the decode kernel sources still hash to the measured version (else null).
+(114,688 B x (pos + 1)) + KV write (114,688 B), times the tokens of a launch, over the per-launch
+duration measured with HIP events on the launch stream, against 8 TB/s.  `traffic` is the HBM
+bytes per launch: the bytes per token measured by two rocprofv3 counter passes (FETCH_SIZE,
+WRITE_SIZE over `--pmc-workload`, scaled by what the same counters read for a 256 MiB copy),
+taken from the committed profile summary, times the tokens of a launch; reported only while the
+decode kernel sources still hash to the measured version (else null).
 
 cpu_baseline: the CPU oracle (oracle/ref_cpu.py, PyTorch fp32 restatement of the reference decode
 path) on BASELINE config 1 (16-token prompt fed through decode, then 32 greedy tokens), timed on
@@ -54,7 +56,7 @@ def decode_source_sha() -> str:
 
 
 def measured_traffic():
-    """HBM bytes per decode launch from the committed FETCH_SIZE / WRITE_SIZE counter passes
+    """HBM bytes per decoded token from the committed FETCH_SIZE / WRITE_SIZE counter passes
     (copy-calibrated), or None when the decode sources changed since they were measured."""
     try:
         kv = dict(line.strip().split(": ", 1) for line in open(TRAFFIC_PROFILE)
@@ -63,7 +65,7 @@ def measured_traffic():
         return None
     if kv.get("source_sha") != decode_source_sha():
         return None
-    return int(kv["traffic_bytes_per_launch"])
+    return int(kv["traffic_bytes_per_token"])
 
 
 def bytes_per_token(pos: int) -> int:
@@ -99,9 +101,14 @@ def build_decoder(max_seq: int, max_prefill: int = 0):
     return dec, spec
 
 
-def time_bucket(dec, start_pos: int, steps: int):
-    """Prefills `start_pos` random tokens, then times `steps` decode launches one by one with
-    event pairs (per-launch duration) inside one region bracketed by synchronize (wall time)."""
+STEPS_PER_LAUNCH = 64     # tokens the persistent kernel chains in one launch (MQ_STEPS_PER_LAUNCH)
+
+
+def time_bucket(dec, start_pos: int, steps: int, per_launch_steps: int = STEPS_PER_LAUNCH):
+    """Prefills `start_pos` random tokens, then times `steps` decode steps as a device-side chain
+    of launches of up to `per_launch_steps` tokens, with an event pair around each launch (launch
+    duration) inside one region bracketed by synchronize (wall time).  Returns (wall seconds,
+    mean seconds per launch, mean tokens per launch)."""
     import torch
     from megaqwen_amd.synthetic import make_tokens
     dec.reset()
@@ -109,24 +116,25 @@ def time_bucket(dec, start_pos: int, steps: int):
     assert dec.position() == start_pos
     buf = torch.empty(steps + 1, dtype=torch.int32, device="cuda")
     buf[0] = tok
+    chunks = [(i, min(per_launch_steps, steps - i)) for i in range(0, steps, per_launch_steps)]
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
+          for _ in chunks]
     lib, h = dec._lib, dec._h
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        ev[i][0].record(stream)
-        rc = lib.mq_decode_steps(h, buf.data_ptr() + 4 * i, 1, sp)
-        ev[i][1].record(stream)
+    for (i, n), (a, b) in zip(chunks, ev):
+        a.record(stream)
+        rc = lib.mq_decode_steps(h, buf.data_ptr() + 4 * i, n, sp)
+        b.record(stream)
         if rc != 0:
             raise RuntimeError(lib.mq_last_error().decode())
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per_launch = sum(a.elapsed_time(b) for a, b in ev) / steps / 1e3
+    per_launch = sum(a.elapsed_time(b) for a, b in ev) / len(ev) / 1e3
     dec.check()
-    return wall, per_launch
+    return wall, per_launch, steps / len(chunks)
 
 
 def time_prefill(dec, n: int, reps: int):
@@ -166,7 +174,7 @@ def pmc_workload():
     torch.cuda.synchronize()
     dec, _ = build_decoder(256, max_prefill=128)
     tok = dec.prefill_step(make_tokens(128, 151936, seed=1))
-    toks = dec.decode_steps_cuda(tok, 16)
+    toks = dec.decode_steps_cuda(tok, 16)          # one persistent launch of 16 chained tokens
     torch.cuda.synchronize()
     dec.check()
     print(f"pmc workload done: 256 MiB copy, prefill 128, decode 16 -> {toks[-1].item()}")
@@ -231,8 +239,8 @@ def main():
     ap.add_argument("--mode", default="persistent", choices=["persistent", "multi_kernel"])
     ap.add_argument("--pmc-workload", action="store_true",
                     help="short fixed workload for hardware-counter runs: a 256 MiB device copy "
-                         "(calibration of FETCH_SIZE / WRITE_SIZE), a 128-token prefill, then 16 "
-                         "decode steps at positions 128..143")
+                         "(calibration of FETCH_SIZE / WRITE_SIZE), a 128-token prefill, then one "
+                         "decode launch of 16 chained steps at positions 128..143")
     ap.add_argument("--prefill-workload", type=int, default=0, metavar="N",
                     help="for counter runs of the prefill kernels: two N-token prefills, nothing else")
     args = ap.parse_args()
@@ -261,17 +269,24 @@ def main():
     torch.cuda.synchronize()
     res = {}
     for p in positions:
-        wall, per_launch = time_bucket(dec, p, K)
+        wall, per_launch, tpl = time_bucket(dec, p, K)
         tok_s = K / wall
         mid = p + (K - 1) / 2
         res[p] = {"tok_s": tok_s, "ms_per_token": 1e3 * wall / K,
-                  "kernel_us": per_launch * 1e6,
+                  "launch_us": per_launch * 1e6, "tokens_per_launch": tpl,
+                  "kernel_us_per_token": per_launch / tpl * 1e6,
                   "bytes_per_token": bytes_per_token(int(mid)),
                   "roofline_frac_wall": bytes_per_token(int(mid)) * tok_s / HBM_PEAK,
-                  "roofline_frac_kernel": bytes_per_token(int(mid)) / per_launch / HBM_PEAK}
-        print(f"[bench] pos {p}: {tok_s:.1f} tok/s, kernel {per_launch * 1e6:.1f} us, "
-              f"roofline {res[p]['roofline_frac_wall'] * 100:.1f}% (wall) "
-              f"{res[p]['roofline_frac_kernel'] * 100:.1f}% (kernel)", file=sys.stderr, flush=True)
+                  "roofline_frac_kernel": bytes_per_token(int(mid)) * tpl / per_launch / HBM_PEAK}
+        print(f"[bench] pos {p}: {tok_s:.1f} tok/s, kernel {per_launch / tpl * 1e6:.1f} us/token "
+              f"({tpl:.0f} tokens per launch), roofline {res[p]['roofline_frac_wall'] * 100:.1f}% "
+              f"(wall) {res[p]['roofline_frac_kernel'] * 100:.1f}% (kernel)", file=sys.stderr,
+              flush=True)
+    # the reference's pattern, one launch per token (bindings_prefill.cpp:1045-1120)
+    wall1, per_launch1, _ = time_bucket(dec, 128, K, per_launch_steps=1)
+    one_launch = {"tok_s": round(K / wall1, 2), "kernel_us": round(per_launch1 * 1e6, 1)}
+    print(f"[bench] pos 128, one launch per token: {one_launch['tok_s']} tok/s, kernel "
+          f"{one_launch['kernel_us']} us", file=sys.stderr, flush=True)
 
     pf_best, pf_mean = time_prefill(dec, 512, 5)
     pf4_best, _ = time_prefill(dec, 4096, 2)
@@ -285,7 +300,8 @@ def main():
           f"4096: {prefill['ms_4096']} ms ({prefill['mfma_util_4096'] * 100:.1f}%)",
           file=sys.stderr, flush=True)
     head = res[128]
-    achieved = head["bytes_per_token"] / (head["kernel_us"] * 1e-6)
+    achieved = head["bytes_per_token"] * head["tokens_per_launch"] / (head["launch_us"] * 1e-6)
+    traffic = measured_traffic() if args.mode == "persistent" else None
     cpu = None
     if not args.no_cpu_baseline:
         del dec
@@ -312,14 +328,18 @@ def main():
                    "tok_s_by_position": {str(p): round(r["tok_s"], 2) for p, r in res.items()},
                    "roofline_frac_by_position": {str(p): round(r["roofline_frac_wall"], 4)
                                                  for p, r in res.items()},
+                   "tokens_per_launch": head["tokens_per_launch"],
+                   "tok_s_one_launch_per_token": one_launch,
                    "prefill": prefill},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 2), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
-                     "traffic": measured_traffic() if args.mode == "persistent" else None,
+                     "traffic": (int(traffic * head["tokens_per_launch"])
+                                 if traffic is not None else None),
                      "kernel": "mq_decode_persistent_kernel" if args.mode == "persistent"
                      else "mq_decode_phase_kernel (all phases)",
-                     "kernel_us": round(head["kernel_us"], 2),
-                     "bytes_per_launch": head["bytes_per_token"]},
+                     "kernel_us": round(head["launch_us"], 2),
+                     "kernel_us_per_token": round(head["kernel_us_per_token"], 2),
+                     "bytes_per_launch": int(head["bytes_per_token"] * head["tokens_per_launch"])},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

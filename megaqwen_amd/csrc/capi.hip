@@ -184,6 +184,7 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   p.s = reinterpret_cast<MqScratch*>(ws + lay.scratch);
   p.st = reinterpret_cast<MqState*>(ws + lay.state);
   p.scale_log2 = (float)(1.4426950408889634 / sqrt((double)MQ_D));
+  p.nsteps = 1;
   dec->lay = lay;
   dec->mode = mode;
   dec->grid = grid;
@@ -312,14 +313,18 @@ int mq_decode_steps(mq_decoder* dec, int32_t* d_tokens, int n, void* stream) {
   if ((long long)dec->pos + n > dec->p.max_seq)
     return fail(MQ_ERR_POSITION, "decode_steps would exceed max_seq_len (%d + %d > %d)",
                 dec->pos, n, dec->p.max_seq);
-  for (int i = 0; i < n; ++i) {
+  // persistent mode: up to MQ_STEPS_PER_LAUNCH tokens per launch (the kernel chains them on the
+  // device); the multi-kernel mode launches its phases per token
+  const int per = dec->mode == MQ_MODE_PERSISTENT ? MQ_STEPS_PER_LAUNCH : 1;
+  for (int i = 0; i < n; i += per) {
     MqDecodeParams p = dec->p;
+    p.nsteps = n - i < per ? n - i : per;
     p.tok_in = d_tokens + i;
     p.tok_out = d_tokens + i + 1;
     p.logits = nullptr;
     int rc = mq_launch_decode(p, dec->mode, dec->grid, static_cast<hipStream_t>(stream));
-    if (rc != 0) return fail(MQ_ERR_HIP, "decode launch %d failed (%d)", i, rc);
-    dec->pos += 1;
+    if (rc != 0) return fail(MQ_ERR_HIP, "decode launch at step %d failed (%d)", i, rc);
+    dec->pos += p.nsteps;
   }
   return MQ_OK;
 }

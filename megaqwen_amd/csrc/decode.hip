@@ -325,7 +325,9 @@ MQ_DEV void attn_prologue(float* lds) {
   }
 }
 
-// Sync wave: the new position's K and V rows (bf16) into the cache of `layer`, kv head h.
+// Sync wave: the new position's K and V rows (bf16) into the cache of `layer`, kv head h.  The
+// stores are device-scope (sc1): within a multi-step launch a workgroup on another XCD reads the
+// row in the next step, and a plain store would sit in this XCD's L2.
 MQ_DEV void attn_cache_row(const MqDecodeParams& p, int layer, int h, int pos, const float* lds) {
   const int lane = lane_id();
   const size_t row = (((size_t)layer * MQ_NKV + h) * p.max_seq + pos) * MQ_D;
@@ -333,8 +335,10 @@ MQ_DEV void attn_cache_row(const MqDecodeParams& p, int layer, int h, int pos, c
                       ((uint32_t)f32_to_bf16(lds[ALDS_KN + 2 * lane + 1]) << 16);
   const uint32_t v2 = (uint32_t)f32_to_bf16(lds[ALDS_VN + 2 * lane]) |
                       ((uint32_t)f32_to_bf16(lds[ALDS_VN + 2 * lane + 1]) << 16);
-  reinterpret_cast<uint32_t*>(p.kc + row)[lane] = k2;
-  reinterpret_cast<uint32_t*>(p.vc + row)[lane] = v2;
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p.kc + row) + lane, k2, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p.vc + row) + lane, v2, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // K/V of up to MQ_ATT_BLOCK positions: position blk + k*28 + wave*4 + (lane/16) goes to compute
@@ -706,7 +710,8 @@ MQ_DEV void down_publish(int wg, int G, const float* lds, float& res, Out out) {
 // is the two-kernel reference equivalent).  Ordering between a workgroup's two atomics comes
 // from waiting for the first to return; no cache-wide fences are used.
 MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int* tok_out,
-                        float* logits, int pos, bool advance_pos, bool round_norm = false) {
+                        float* logits, int pos, bool advance_pos, bool round_norm = false,
+                        bool publish_epoch = false, uint32_t step_epoch = 0) {
   float* xn = lds + LDS_XN;
   uint64_t* keys = reinterpret_cast<uint64_t*>(lds + LDS_KEYS);
   norm_1024(lds + LDS_IN, p.final_norm, xn, lds + LDS_RED, round_norm);
@@ -760,7 +765,9 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
     if (old == (uint32_t)G - 1) {
       const unsigned long long kk =
           __hip_atomic_load(&sy->argmax.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *tok_out = (int)argmax_key_index(kk);
+      // device-scope store: the next step of a multi-step launch reads it in other workgroups
+      __hip_atomic_store(reinterpret_cast<uint32_t*>(tok_out), argmax_key_index(kk),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&sy->argmax.v, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       for (int i = 0; i < MQ_BAR_STRIPES; ++i)
         __hip_atomic_store(&sy->bar[i].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -770,6 +777,11 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
         __hip_atomic_store(&p.st->pos.v, (uint32_t)(pos + 1), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&sy->done.v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (publish_epoch) {
+        // every reset above and the token are complete before the epoch releases the next step
+        wait_all_memory();
+        __hip_atomic_store(&p.st->steps.v, step_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
 }
@@ -1018,12 +1030,13 @@ MQ_DEV void phase_step(Epi epilogue, Arrive arrive, Prefetch prefetch, Wait wait
 // ------------------------------------------------------------------------------- kernels
 // Reads and validates the step's position and input token.  The result is identical in every
 // workgroup, so an invalid step makes all of them return before the first barrier.
-MQ_DEV bool step_inputs(const MqDecodeParams& p, int& pos, int& tok) {
+MQ_DEV bool step_inputs(const MqDecodeParams& p, const int* tok_in, int& pos, int& tok) {
   // uniform by construction; readfirstlane lets the compiler treat everything derived from them
   // as scalar (uniform branches, no per-lane copies of alternative code paths)
   pos = __builtin_amdgcn_readfirstlane(
       (int)__hip_atomic_load(&p.st->pos.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  tok = __builtin_amdgcn_readfirstlane(*p.tok_in);
+  tok = __builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
+      reinterpret_cast<const uint32_t*>(tok_in), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   if (pos < 0 || pos >= p.max_seq || tok < 0 || tok >= p.vocab) {
     if (blockIdx.x == 0 && tid() == 0)
       __hip_atomic_store(&p.st->sync.err.v, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1061,12 +1074,36 @@ MQ_DEV MqLayerW lds_layer(const MqLayerW* table, int l) {
 }
 static_assert(sizeof(MqLayerW) == 11 * sizeof(void*), "MqLayerW holds exactly the 11 pointers");
 
+// Sync wave: waits until the multi-step epoch reaches `target` (the last workgroup of a step
+// publishes it after resetting the step's sync state), then the workgroup proceeds.
+MQ_DEV void step_wait(const MqDecodeParams& p, uint32_t target) {
+  __syncthreads();
+  if (wave_id() == MQ_SYNC_WAVE) {
+    const int lane = lane_id();
+    uint32_t spins = 0;
+    while (true) {
+      uint32_t v = 0;
+      if (lane == 0)
+        v = __hip_atomic_load(&p.st->steps.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else if (lane == 63)
+        v = __hip_atomic_load(&p.st->sync.err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t e = __builtin_amdgcn_readlane(v, 63);
+      const uint32_t c = __builtin_amdgcn_readlane(v, 0);
+      if (e != 0 || (int32_t)(c - target) >= 0) break;
+      if (++spins > MQ_SPIN_LIMIT) {
+        if (lane == 0)
+          __hip_atomic_store(&p.st->sync.err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
 __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDecodeParams p) {
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   __shared__ MqLayerW s_layers[MQ_MAX_LAYERS];
   const int G = gridDim.x, wg = blockIdx.x;
-  int pos, tok;
-  if (!step_inputs(p, pos, tok)) return;
   {
     const int nw = p.num_layers * (int)(sizeof(MqLayerW) / 4);
     for (int i = tid(); i < nw; i += MQ_THREADS)
@@ -1074,85 +1111,100 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     __syncthreads();
   }
   const int h = wg % MQ_GROUPS, j = wg / MQ_GROUPS, NG = G / MQ_GROUPS;
-  const GAttn ga = gattn_plan(j, NG, pos + 1, pos);
   MqSync* sy = &p.st->sync;
   MqScratch* s = p.s;
-  const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
-  const bf16_t* cs = p.cos + (size_t)pos * MQ_D;
-  const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
   int r0h, nrh;
   row_range(MQ_H, wg, G, r0h, nrh);
-  uint32_t nbar = 0;
+  // the step-done epoch before this launch: read by every workgroup before any can complete the
+  // first step (completion needs every workgroup's arrival at the LM head)
+  const uint32_t epoch0 = __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(&p.st->steps.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   QkvSet wq;
   OPairSet wo;
   GateUpSet wgu;
   DownSet wd;
   KvBlock kv;
   if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG);
-  phase_step(MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
-  for (int l = 0; l < p.num_layers; ++l) {
-    const MqLayerW w = lds_layer(s_layers, l);
-    stamp(p, wg, l, 0);
-    // this layer's K/V chunk: issued before the q|k|v dot products so that it arrives during
-    // them and the group barrier (the group barrier alone is shorter than an HBM round trip)
-    if (ga.active) {
-      kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
-                    min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
+  for (int step = 0; step < p.nsteps; ++step) {
+    int pos, tok;
+    if (!step_inputs(p, step == 0 ? p.tok_in : p.tok_out + (step - 1), pos, tok)) return;
+    const GAttn ga = gattn_plan(j, NG, pos + 1, pos);
+    const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
+    const bf16_t* cs = p.cos + (size_t)pos * MQ_D;
+    const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
+    uint32_t nbar = 0;
+    phase_step(MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
+    for (int l = 0; l < p.num_layers; ++l) {
+      const MqLayerW w = lds_layer(s_layers, l);
+      stamp(p, wg, l, 0);
+      // this layer's K/V chunk: issued before the q|k|v dot products so that it arrives during
+      // them and the group barrier (the group barrier alone is shorter than an HBM round trip)
+      if (ga.active) {
+        kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
+                      min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
+      }
+      gqkv_run(wq, w, h, j, NG, lds);
+      stamp(p, wg, l, 1);
+      // the gate|up weights go out two phases ahead, during the attention phase, from workgroups
+      // without an attention chunk; the others issue them once they have arrived at the grid
+      // barrier after the O projection (a deep queue stalls the issue of loads and would delay
+      // their attention, the partial merge and the O projection, which are on the critical path)
+      phase_step([&] { gqkv_publish(s->qkv, h, j, NG, lds); },
+                 [&] { group_barrier_arrive(sy, h); },
+                 [&] { if (!ga.active) gu_load(wgu, w, wg, G); },
+                 [&] { group_barrier_wait(sy, h, (uint32_t)((2 * l + 1) * NG)); },
+                 [&] { if (ga.active) attn_input(s->qkv, w.q_norm, w.k_norm, cs, sn, h, lds); });
+      stamp(p, wg, l, 2);
+      if (ga.active) {
+        attn_prologue(lds);
+        __syncthreads();
+        attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds, ga.small);
+      }
+      stamp(p, wg, l, 3);
+      phase_step([&] { if (ga.active) gattn_publish(p, l, pos, h, j, ga, lds); },
+                 [&] { group_barrier_arrive(sy, h); },
+                 [&] { opart_load(wo, w, h, j, NG); },
+                 [&] { group_barrier_wait(sy, h, (uint32_t)((2 * l + 2) * NG)); }, MQ_NOTHING);
+      stamp(p, wg, l, 4);
+      group_merge(s->part, h, ga.nch, lds);
+      opart_run(wo, w, h, j, NG, lds);
+      stamp(p, wg, l, 5);
+      phase_step([&] { opart_publish(&s->opart[0][0], h, j, NG, lds); },
+                 [&] { grid_barrier_arrive(sy); },
+                 [&] { if (ga.active) gu_load(wgu, w, wg, G); },
+                 [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); }, MQ_NOTHING);
+      gu_input_all(&s->opart[0][0], lds);
+      stamp(p, wg, l, 6);
+      gu_run(wgu, w, wg, G, lds);
+      stamp(p, wg, l, 7);
+      phase_step([&] { gu_publish(s->mlp, wg, G, lds); },
+                 [&] { grid_barrier_arrive(sy); },
+                 [&] { down_load(wd, w, wg, G); },
+                 [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); },
+                 [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, s->mlp); });
+      stamp(p, wg, l, 8);
+      down_run(wd, w, wg, G, lds);
+      stamp(p, wg, l, 9);
+      phase_step(
+          [&] {
+            float res = lane_id() < nrh ? lds[LDS_A + r0h + lane_id()] : 0.f;
+            down_publish(wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); });
+          },
+          [&] { grid_barrier_arrive(sy); },
+          [&] { if (l + 1 < p.num_layers) gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG); },
+          [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); },
+          [&] { input_hidden_coh(lds, s->hidden); });
+      stamp(p, wg, l, 10);
     }
-    gqkv_run(wq, w, h, j, NG, lds);
-    stamp(p, wg, l, 1);
-    // the gate|up weights go out two phases ahead, during the attention phase, from workgroups
-    // without an attention chunk; the others issue them once they have arrived at the grid
-    // barrier after the O projection (a deep queue stalls the issue of loads and would delay
-    // their attention, the partial merge and the O projection, which are on the critical path)
-    phase_step([&] { gqkv_publish(s->qkv, h, j, NG, lds); },
-               [&] { group_barrier_arrive(sy, h); },
-               [&] { if (!ga.active) gu_load(wgu, w, wg, G); },
-               [&] { group_barrier_wait(sy, h, (uint32_t)((2 * l + 1) * NG)); },
-               [&] { if (ga.active) attn_input(s->qkv, w.q_norm, w.k_norm, cs, sn, h, lds); });
-    stamp(p, wg, l, 2);
-    if (ga.active) {
-      attn_prologue(lds);
-      __syncthreads();
-      attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds, ga.small);
+    const bool more = step + 1 < p.nsteps;
+    lm_head_run(p, wg, G, lds, p.tok_out + step, p.nsteps == 1 ? p.logits : nullptr, pos, true,
+                false, more, epoch0 + (uint32_t)step + 1);
+    if (more) {
+      // the next step's first weights do not depend on its token: in flight during the wait
+      if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG);
+      step_wait(p, epoch0 + (uint32_t)step + 1);
     }
-    stamp(p, wg, l, 3);
-    phase_step([&] { if (ga.active) gattn_publish(p, l, pos, h, j, ga, lds); },
-               [&] { group_barrier_arrive(sy, h); },
-               [&] { opart_load(wo, w, h, j, NG); },
-               [&] { group_barrier_wait(sy, h, (uint32_t)((2 * l + 2) * NG)); }, MQ_NOTHING);
-    stamp(p, wg, l, 4);
-    group_merge(s->part, h, ga.nch, lds);
-    opart_run(wo, w, h, j, NG, lds);
-    stamp(p, wg, l, 5);
-    phase_step([&] { opart_publish(&s->opart[0][0], h, j, NG, lds); },
-               [&] { grid_barrier_arrive(sy); },
-               [&] { if (ga.active) gu_load(wgu, w, wg, G); },
-               [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); }, MQ_NOTHING);
-    gu_input_all(&s->opart[0][0], lds);
-    stamp(p, wg, l, 6);
-    gu_run(wgu, w, wg, G, lds);
-    stamp(p, wg, l, 7);
-    phase_step([&] { gu_publish(s->mlp, wg, G, lds); },
-               [&] { grid_barrier_arrive(sy); },
-               [&] { down_load(wd, w, wg, G); },
-               [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); },
-               [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, s->mlp); });
-    stamp(p, wg, l, 8);
-    down_run(wd, w, wg, G, lds);
-    stamp(p, wg, l, 9);
-    phase_step(
-        [&] {
-          float res = lane_id() < nrh ? lds[LDS_A + r0h + lane_id()] : 0.f;
-          down_publish(wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); });
-        },
-        [&] { grid_barrier_arrive(sy); },
-        [&] { if (l + 1 < p.num_layers) gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG); },
-        [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); },
-        [&] { input_hidden_coh(lds, s->hidden); });
-    stamp(p, wg, l, 10);
   }
-  lm_head_run(p, wg, G, lds, p.tok_out, p.logits, pos, true);
 }
 
 // One kernel per phase of the head-group step (kernel boundaries replace the barriers).  Every
@@ -1163,7 +1215,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   const int G = gridDim.x, wg = blockIdx.x;
   int pos, tok;
-  if (!step_inputs(p, pos, tok)) return;
+  if (!step_inputs(p, p.tok_in, pos, tok)) return;
   MqScratch* s = p.s;
   MqSync* sy = &p.st->sync;
   const int h = wg % MQ_GROUPS, j = wg / MQ_GROUPS, NG = G / MQ_GROUPS;
@@ -1350,6 +1402,7 @@ __global__ void mq_fill_state_kernel(MqState* st, int pos) {
     st->sync.err.v = 0;
     st->sync.argmax.v = 0;
     st->pos.v = (uint32_t)pos;
+    st->steps.v = 0;
   }
 }
 __global__ void mq_zero_kernel(uint4* p, size_t n16) {

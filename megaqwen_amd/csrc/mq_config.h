@@ -22,6 +22,7 @@
 #define MQ_MAX_CHUNKS 64                // attention split-K chunks per kv head (upper bound)
 #define MQ_MAX_LAYERS 64                // decoder layers (the persistent kernel keeps their
                                         // weight-pointer table in LDS)
+#define MQ_STEPS_PER_LAUNCH 64          // decode_steps: tokens chained inside one persistent launch
 #define MQ_PART_STRIDE 132              // floats per attention partial: m, l, pad, pad, o[128]
 #define MQ_ATT_NK 8                     // positions per compute-wave row per attention block
 #define MQ_ATT_BLOCK (4 * MQ_CWAVES * MQ_ATT_NK)   // 224 positions scored per pass of a chunk

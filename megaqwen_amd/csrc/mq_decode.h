@@ -41,6 +41,7 @@ struct MqScratch {
 struct MqState {
   MqSync sync;
   MqLine pos;                  // device-side decode position (read at step start, +1 at step end)
+  MqLine steps;                // completed steps of multi-step launches (the step-done epoch)
 };
 
 struct MqDecodeParams {
@@ -63,6 +64,9 @@ struct MqDecodeParams {
   MqScratch* s;
   MqState* st;
   float scale_log2;            // log2(e) / sqrt(D): scores are kept in the log2 domain
+  int nsteps;                  // persistent mode: tokens decoded by one launch.  Step i reads
+                               // tok_in (i = 0) or tok_out[i - 1] and writes tok_out[i]; logits
+                               // are written for nsteps == 1 only
 };
 
 // Per-layer timestamps of the persistent kernel's debug mode (s_memrealtime, 100 MHz):

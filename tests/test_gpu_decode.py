@@ -225,6 +225,31 @@ def test_decode_steps_chain_and_graph(small):
     dec.check()
 
 
+def test_multi_step_launch_matches_single_steps(small):
+    """decode_steps chains up to 64 tokens inside one persistent launch (the next step's token,
+    position, KV row and sync state pass between workgroups on the device).  70 steps cross a
+    launch boundary; tokens, every KV-cache row and the next step's logits equal the one-launch-
+    per-token path bit for bit."""
+    dec, _, sp, _ = small
+    first = int(make_tokens(1, sp["vocab_size"], seed=12)[0])
+    dec.set_mode("persistent")
+    dec.reset()
+    ref, t = [], first
+    for _ in range(70):
+        t = dec.decode_step(t)
+        ref.append(t)
+    kref, vref = dec.k_cache.clone(), dec.v_cache.clone()
+    tref, lref = dec.decode_step_with_logits(ref[-1])
+    dec.reset()
+    chain = dec.decode_steps_cuda(first, 70).cpu().tolist()
+    assert chain == ref and dec.position() == 70
+    assert torch.equal(dec.k_cache[:, :, :70], kref[:, :, :70])
+    assert torch.equal(dec.v_cache[:, :, :70], vref[:, :, :70])
+    tok, lg = dec.decode_step_with_logits(chain[-1])
+    assert tok == tref and torch.equal(lg, lref)
+    dec.check()
+
+
 def test_decode_greedy_cuda_eos(small):
     dec, _, sp, _ = small
     first = int(make_tokens(1, sp["vocab_size"], seed=7)[0])
