@@ -130,7 +130,8 @@ int mq_decode_step(mq_decoder* dec, const int32_t* d_token_in, int32_t* d_token_
 /* decode_steps_cuda (bindings_prefill.cpp:1045-1075): d_tokens[0] holds the first token;
  * step i reads d_tokens[i] and writes d_tokens[i+1], i < n.  The chain stays on the device, so
  * it also replaces the reference's fill_iota + first-EOS helpers
- * (fused_decode_ldg_launch.inl:5-53) that decode_greedy_cuda builds on. */
+ * (fused_decode_ldg_launch.inl:5-53) that decode_greedy_cuda builds on.  In the persistent mode
+ * one kernel launch decodes up to 64 chained tokens (the reference launches once per token). */
 int mq_decode_steps(mq_decoder* dec, int32_t* d_tokens, int n, void* stream);
 
 /* Debug hook (the reference's counterpart is debug_ldg_decode_cycles,
