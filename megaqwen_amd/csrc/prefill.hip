@@ -182,9 +182,9 @@ struct GemmArgs {
   int M, N, K;
 };
 
-#define GEMM_BK 64
-#define GEMM_LDS_STRIDE 72   // bf16 per LDS row: 64 + 8 padding (16-byte chunk c of row r at 9r + c)
-#define GEMM_STAGES 4        // K steps whose global loads are in flight in registers (64-row tiles)
+#define GEMM_BK 64           // K per step of 64- and 128-row tiles (32-row tiles: 128)
+#define GEMM_STAGES 4        // K steps whose global loads are in flight in registers (64-row and
+                             // 32-row tiles)
 #define GEMM_STAGES_BIG 2    // the same for 128-row tiles, so two of their waves fit on a SIMD
 
 // One BM x BN tile of C per workgroup of 4 waves, K in steps of 64.  The global loads of step
@@ -203,14 +203,20 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
   constexpr int WM = KG == 2 ? 32 : BM / 2;       // rows of a wave's tile
   constexpr int WN = BN / 2;                      // columns of a wave's tile
   constexpr int MB = WM / 32, NBK = WN / 32;      // 32 x 32 MFMA blocks per wave tile
-  constexpr int NA = BM / 32;                     // 16-byte A loads per thread per step
-  constexpr int NL = BN / 32;                     // 16-byte loads per weight tile per thread
+  constexpr int BK = BM == 32 ? 128 : GEMM_BK;    // K per step (32-row tiles: fewer, longer steps)
+  constexpr int LDSS = BK + 8;                    // bf16 per LDS row (16-byte chunk c of row r at
+                                                  // (BK / 8 + 1) r + c: conflict-free reads)
+  constexpr int CPR = BK / 8;                     // 16-byte chunks per tile row and step
+  constexpr int RPP = 256 / CPR;                  // rows staged per pass of the 256 threads
+  constexpr int NA = BM / RPP;                    // 16-byte A loads per thread per step
+  constexpr int NL = BN / RPP;                    // 16-byte loads per weight tile per thread
+  constexpr int KQ = BK / 16;                     // MFMA k-steps per step
   constexpr int S = BM == 128 ? GEMM_STAGES_BIG : GEMM_STAGES;
   static_assert(BM == 32 || BM == 64 || BM == 128, "tile rows");
   static_assert(BN == 64 || BN == 128, "tile columns");
   static_assert(KG == 1 || BN == 64, "the K-split layout covers 32 x 64 tiles");
-  __shared__ __align__(16) bf16_t As[2][BM * GEMM_LDS_STRIDE];
-  __shared__ __align__(16) bf16_t Bs[2][NB][BN * GEMM_LDS_STRIDE];
+  __shared__ __align__(16) bf16_t As[2][BM * LDSS];
+  __shared__ __align__(16) bf16_t Bs[2][NB][BN * LDSS];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wn = wave & 1;
   const int wm = KG == 1 ? (wave >> 1) : 0;
@@ -222,13 +228,13 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
   else B = g.B2 + (size_t)(n_base - g.n1) * g.K;
   const bf16_t* Bu = (EPI == EPI_SWIGLU) ? g.Bu + (size_t)n_base * g.K : B;
 
-  // global -> register staging: thread t moves 16-byte chunk t % 8 of rows t / 8 + 32 i.
+  // global -> register staging: thread t moves 16-byte chunk t % CPR of rows t / CPR + RPP i.
   // Rows past M read row M - 1 (their results are never stored).
-  const int sr = t >> 3, sk = (t & 7) * 8;
+  const int sr = t / CPR, sk = (t % CPR) * 8;
   const bf16_t* a_src[NA];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    const int am = min(m_base + sr + 32 * i, g.M - 1);
+    const int am = min(m_base + sr + RPP * i, g.M - 1);
     a_src[i] = g.A + (size_t)am * g.lda + sk;
   }
   const bf16_t* b_src[NB];
@@ -237,23 +243,23 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
 
   uint4 ra[S][NA], rb[S][NB][NL];
   auto load_step = [&](int k, uint4 (&a)[NA], uint4 (&b)[NB][NL]) {
-    const int k0 = k * GEMM_BK;
+    const int k0 = k * BK;
 #pragma unroll
     for (int i = 0; i < NA; ++i) a[i] = ld16(a_src[i] + k0);
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int i = 0; i < NL; ++i) b[j][i] = ld16(b_src[j] + (size_t)(32 * i) * g.K + k0);
+      for (int i = 0; i < NL; ++i) b[j][i] = ld16(b_src[j] + (size_t)(RPP * i) * g.K + k0);
   };
   auto store_step = [&](int buf, const uint4 (&a)[NA], const uint4 (&b)[NB][NL]) {
 #pragma unroll
     for (int i = 0; i < NA; ++i)
-      *reinterpret_cast<uint4*>(&As[buf][(sr + 32 * i) * GEMM_LDS_STRIDE + sk]) = a[i];
+      *reinterpret_cast<uint4*>(&As[buf][(sr + RPP * i) * LDSS + sk]) = a[i];
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int i = 0; i < NL; ++i)
-        *reinterpret_cast<uint4*>(&Bs[buf][j][(sr + 32 * i) * GEMM_LDS_STRIDE + sk]) = b[j][i];
+        *reinterpret_cast<uint4*>(&Bs[buf][j][(sr + RPP * i) * LDSS + sk]) = b[j][i];
   };
 
   mq_f32x16 acc[NB][MB][NBK];
@@ -269,19 +275,19 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
   const int fr = lane & 31, fk = (lane >> 5) * 8;   // MFMA operand row and k offset of a lane
   auto mma_step = [&](int buf) {
 #pragma unroll
-    for (int q = 0; q < 4 / KG; ++q) {
-      const int kofs = 16 * (q + wk * (4 / KG)) + fk;
+    for (int q = 0; q < KQ / KG; ++q) {
+      const int kofs = 16 * (q + wk * (KQ / KG)) + fk;
       mq_bf16x8 af[MB];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
         af[mb] = as_bf16x8(*reinterpret_cast<const uint4*>(
-            &As[buf][(wm * WM + mb * 32 + fr) * GEMM_LDS_STRIDE + kofs]));
+            &As[buf][(wm * WM + mb * 32 + fr) * LDSS + kofs]));
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int nb = 0; nb < NBK; ++nb) {
           const mq_bf16x8 bf = as_bf16x8(*reinterpret_cast<const uint4*>(
-              &Bs[buf][b][(wn * WN + nb * 32 + fr) * GEMM_LDS_STRIDE + kofs]));
+              &Bs[buf][b][(wn * WN + nb * 32 + fr) * LDSS + kofs]));
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb)
             acc[b][mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], bf, acc[b][mb][nb],
@@ -293,8 +299,9 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
   // Schedule (all slot and buffer indices compile-time, so each step is straight-line code and
   // the loads of a slot are waited for only when that slot is stored): step k stores slot
   // (k + 1) % S into LDS buffer (k + 1) % 2, refills slot k % S with step k + S and multiplies
-  // buffer k % 2.  K / 64 is a multiple of S (checked by the host).
-  const int nk = g.K / GEMM_BK;
+  // buffer k % 2.  K / BK is a multiple of S (every K of the model is a multiple of 512, see the
+  // static_assert at the launcher).
+  const int nk = g.K / BK;
 #pragma unroll
   for (int s = 0; s < S; ++s) load_step(s, ra[s], rb[s]);
   store_step(0, ra[0], rb[0]);
@@ -612,7 +619,9 @@ void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n) {
   b->kt = reinterpret_cast<bf16_t*>(c);
 }
 
-// K must be a multiple of 256 and N of 128 (every Qwen3-0.6B projection is).  Tile choice:
+// K must be a multiple of 512 and N of 128 (every Qwen3-0.6B projection is).
+static_assert(MQ_H % 512 == 0 && MQ_QDIM % 512 == 0 && MQ_I % 512 == 0, "GEMM K steps");
+// Tile choice:
 // 128 x 128 (128 x 64 for the two SwiGLU matrices) when that still gives >= 512 workgroups
 // (two per CU; large M); otherwise 64 x 64, or 32 x 64 when even 64-row tiles would leave CUs
 // idle (the N = 1024 GEMMs at M <= 1024).
