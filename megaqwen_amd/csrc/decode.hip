@@ -207,7 +207,7 @@ MQ_DEV void norm_1024(const float* x, const bf16_t* __restrict__ w, float* xn, f
   const float2 v = reinterpret_cast<const float2*>(x)[t];
   const float ss = block_sum(v.x * v.x + v.y * v.y, red);
   const float r = rsqrtf(ss * (1.0f / MQ_H) + MQ_EPS);
-  const uint32_t wv = reinterpret_cast<const uint32_t*>(w)[t];
+  const uint32_t wv = ld32(w + 2 * t);
   float y0 = v.x * r * bf16_lo(wv), y1 = v.y * r * bf16_hi(wv);
   if (round_out) {
     y0 = round_bf16(y0);
@@ -289,10 +289,10 @@ MQ_DEV void attn_input(const float* qkv, const bf16_t* qn, const bf16_t* kn, con
   v[2] = ld_coh2(qkv + MQ_QDIM + h * MQ_D + 2 * lane);
   v[3] = ld_coh2(qkv + MQ_QDIM + MQ_KVDIM + h * MQ_D + 2 * lane);
   uint32_t prm[4];
-  prm[0] = reinterpret_cast<const uint32_t*>(qn)[lane];
-  prm[1] = reinterpret_cast<const uint32_t*>(kn)[lane];
-  prm[2] = reinterpret_cast<const uint32_t*>(cs)[lane];
-  prm[3] = reinterpret_cast<const uint32_t*>(sn)[lane];
+  prm[0] = ld32(qn + 2 * lane);
+  prm[1] = ld32(kn + 2 * lane);
+  prm[2] = ld32(cs + 2 * lane);
+  prm[3] = ld32(sn + 2 * lane);
 #pragma unroll
   for (int i = 0; i < 4; ++i) reinterpret_cast<float2*>(lds + ALDS_RAW)[lane + 64 * i] = v[i];
 #pragma unroll

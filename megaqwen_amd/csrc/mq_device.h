@@ -31,12 +31,25 @@ MQ_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 // ---------------------------------------------------------------------------- loads
 // Weights are streamed once per token and never fit in the 256 MB MALL next to the KV cache,
 // so they are loaded non-temporally (no L2 allocation priority).
+// Every pointer these helpers take is global memory.  They load through the global address
+// space explicitly: a pointer whose origin the compiler cannot trace (the weight table is read
+// from LDS) would otherwise be loaded with FLAT instructions, which also count in lgkmcnt, so the
+// next LDS wait or barrier of the wave would wait for the whole weight prefetch to land.
+#define MQ_GLOBAL __attribute__((address_space(1)))
 typedef unsigned int mq_u32x4 __attribute__((ext_vector_type(4)));
+template <class T>
+MQ_DEV const MQ_GLOBAL T* gptr(const void* p) {
+  return (const MQ_GLOBAL T*)(p);
+}
 MQ_DEV uint4 ld_nt16(const void* p) {
-  const mq_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const mq_u32x4*>(p));
+  const mq_u32x4 v = __builtin_nontemporal_load(gptr<mq_u32x4>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
-MQ_DEV uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+MQ_DEV uint4 ld16(const void* p) {
+  const mq_u32x4 v = *gptr<mq_u32x4>(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+MQ_DEV uint32_t ld32(const void* p) { return *gptr<uint32_t>(p); }
 
 // dot of 8 bf16 (one 16-byte load) with 8 fp32 values
 MQ_DEV float dot8(uint4 w, const float* x, float acc) {
