@@ -1137,21 +1137,24 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     for (int l = 0; l < p.num_layers; ++l) {
       const MqLayerW w = lds_layer(s_layers, l);
       stamp(p, wg, l, 0);
-      // this layer's K/V chunk: issued before the q|k|v dot products so that it arrives during
-      // them and the group barrier (the group barrier alone is shorter than an HBM round trip)
-      if (ga.active) {
-        kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
-                      min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
-      }
       gqkv_run(wq, w, h, j, NG, lds);
       stamp(p, wg, l, 1);
       // the gate|up weights go out two phases ahead, during the attention phase, from workgroups
       // without an attention chunk; the others issue them once they have arrived at the grid
       // barrier after the O projection (a deep queue stalls the issue of loads and would delay
-      // their attention, the partial merge and the O projection, which are on the critical path)
+      // their attention, the partial merge and the O projection, which are on the critical path).
+      // Workgroups with a chunk issue its K/V rows here instead, after arriving: issued before
+      // the q|k|v dot products (whose loads are conditional), they made the compiler's wait for
+      // the q|k|v weights wait for them too.
       phase_step([&] { gqkv_publish(s->qkv, h, j, NG, lds); },
                  [&] { group_barrier_arrive(sy, h); },
-                 [&] { if (!ga.active) gu_load(wgu, w, wg, G); },
+                 [&] {
+                   if (!ga.active)
+                     gu_load(wgu, w, wg, G);
+                   else
+                     kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
+                                   min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
+                 },
                  [&] { group_barrier_wait(sy, h, (uint32_t)((2 * l + 1) * NG)); },
                  [&] { if (ga.active) attn_input(s->qkv, w.q_norm, w.k_norm, cs, sn, h, lds); });
       stamp(p, wg, l, 2);
