@@ -272,6 +272,28 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) acc[b][mb][nb][j] = 0.f;
 
+  // EPI_RESID: the residual values of this lane's accumulator elements, loaded now so that the
+  // epilogue does not start with a memory round trip (element (mb, nb, j): row 32 mb + 8 (j / 4) +
+  // 4 (lane / 32) + j % 4, column 32 nb + lane % 32 of the wave's tile; rows past M read row M - 1)
+  // (64-row and smaller tiles; the 128-row tiles have no registers to spare)
+  constexpr bool RPRE = EPI == EPI_RESID && BM <= 64;
+  bf16_t rres[RPRE ? MB : 1][RPRE ? NBK : 1][16];
+  if constexpr (RPRE) {
+    if (KG == 1 || wk == 0) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NBK; ++nb) {
+          const int col = n_base + wn * WN + nb * 32 + (lane & 31);
+          const int rbase = m_base + wm * WM + mb * 32;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int row = min(rbase + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3), g.M - 1);
+            rres[mb][nb][j] = *gptr<bf16_t>(g.R + (size_t)row * g.ldr + col);
+          }
+        }
+    }
+  }
   const int fr = lane & 31, fk = (lane >> 5) * 8;   // MFMA operand row and k offset of a lane
   auto mma_step = [&](int buf) {
 #pragma unroll
@@ -351,7 +373,9 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
           if (EPI == EPI_STORE) {
             v = acc[0][mb][nb][j];
           } else if (EPI == EPI_RESID) {
-            v = round_bf16(acc[0][mb][nb][j]) + bf16_to_f32(g.R[(size_t)row * g.ldr + col]);
+            const bf16_t r = RPRE ? rres[RPRE ? mb : 0][RPRE ? nb : 0][j]
+                                  : g.R[(size_t)row * g.ldr + col];
+            v = round_bf16(acc[0][mb][nb][j]) + bf16_to_f32(r);
           } else {
             const float gv = round_bf16(acc[0][mb][nb][j]), uv = round_bf16(acc[NB - 1][mb][nb][j]);
             v = silu_f(gv) * uv;
