@@ -79,6 +79,7 @@ __global__ void __launch_bounds__(128) pf_rmsnorm_kernel(const bf16_t* __restric
   __shared__ float red[2];
   const int row = blockIdx.x, t = threadIdx.x;
   const uint4 xv = reinterpret_cast<const uint4*>(x + (size_t)row * MQ_H)[t];
+  const uint4 wq = reinterpret_cast<const uint4*>(w)[t];   // loaded with x: one round trip
   float v[8];
   unpack8(xv, v);
   float ss = 0.f;
@@ -89,7 +90,7 @@ __global__ void __launch_bounds__(128) pf_rmsnorm_kernel(const bf16_t* __restric
   __syncthreads();
   const float r = rsqrtf((red[0] + red[1]) * (1.0f / MQ_H) + MQ_EPS);
   float wv[8];
-  unpack8(reinterpret_cast<const uint4*>(w)[t], wv);
+  unpack8(wq, wv);
   uint32_t o[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
@@ -105,18 +106,34 @@ __global__ void __launch_bounds__(128) pf_rmsnorm_kernel(const bf16_t* __restric
 // lane i = lane % 16 dims 4i .. 4i + 3 and their RoPE partners 64 + 4i .. 64 + 4i + 3 (8-byte
 // accesses).
 __global__ void __launch_bounds__(64) pf_qk_norm_rope_kernel(MqDecodeParams p, int layer,
+                                                             const bf16_t* __restrict__ q_norm,
+                                                             const bf16_t* __restrict__ k_norm,
                                                              bf16_t* __restrict__ qkv,
                                                              bf16_t* __restrict__ kt, int ntiles) {
   const int pos = blockIdx.x, lane = threadIdx.x, i = lane & 15;
   const int head = 4 * blockIdx.y + (lane >> 4);
-  const MqLayerW w = p.layers[layer];
   bf16_t* row = qkv + (size_t)pos * MQ_QKV;
   const bool is_q = head < MQ_NQ;
   const int h = is_q ? head : head - MQ_NQ;
   bf16_t* x = row + (is_q ? h * MQ_D : MQ_QDIM + h * MQ_D);
   const int d0 = 4 * i;
+  // every load first (one memory round trip): the head's values, its norm weights, the RoPE row
+  // and, for k heads, the v values that go to the cache
+  const bf16_t* nw = is_q ? q_norm : k_norm;
+  const bf16_t* v = row + MQ_QDIM + MQ_KVDIM + h * MQ_D;
   const uint2 xl = *reinterpret_cast<const uint2*>(x + d0);
   const uint2 xh = *reinterpret_cast<const uint2*>(x + 64 + d0);
+  const uint2 nl = *reinterpret_cast<const uint2*>(nw + d0);
+  const uint2 nh = *reinterpret_cast<const uint2*>(nw + 64 + d0);
+  const uint2 cl = *reinterpret_cast<const uint2*>(p.cos + (size_t)pos * MQ_D + d0);
+  const uint2 ch = *reinterpret_cast<const uint2*>(p.cos + (size_t)pos * MQ_D + 64 + d0);
+  const uint2 sl = *reinterpret_cast<const uint2*>(p.sin + (size_t)pos * MQ_D + d0);
+  const uint2 sh = *reinterpret_cast<const uint2*>(p.sin + (size_t)pos * MQ_D + 64 + d0);
+  uint2 vl = make_uint2(0, 0), vh = make_uint2(0, 0);
+  if (!is_q) {
+    vl = *reinterpret_cast<const uint2*>(v + d0);
+    vh = *reinterpret_cast<const uint2*>(v + 64 + d0);
+  }
   const float lo[4] = {bf16_lo(xl.x), bf16_hi(xl.x), bf16_lo(xl.y), bf16_hi(xl.y)};
   const float hi[4] = {bf16_lo(xh.x), bf16_hi(xh.x), bf16_lo(xh.y), bf16_hi(xh.y)};
   float ss = 0.f;
@@ -124,13 +141,6 @@ __global__ void __launch_bounds__(64) pf_qk_norm_rope_kernel(MqDecodeParams p, i
   for (int e = 0; e < 4; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
   ss = row16_sum(ss);
   const float r = rsqrtf(ss * (1.0f / MQ_D) + MQ_EPS);
-  const bf16_t* nw = is_q ? w.q_norm : w.k_norm;
-  const uint2 nl = *reinterpret_cast<const uint2*>(nw + d0);
-  const uint2 nh = *reinterpret_cast<const uint2*>(nw + 64 + d0);
-  const uint2 cl = *reinterpret_cast<const uint2*>(p.cos + (size_t)pos * MQ_D + d0);
-  const uint2 ch = *reinterpret_cast<const uint2*>(p.cos + (size_t)pos * MQ_D + 64 + d0);
-  const uint2 sl = *reinterpret_cast<const uint2*>(p.sin + (size_t)pos * MQ_D + d0);
-  const uint2 sh = *reinterpret_cast<const uint2*>(p.sin + (size_t)pos * MQ_D + 64 + d0);
   const float nwl[4] = {bf16_lo(nl.x), bf16_hi(nl.x), bf16_lo(nl.y), bf16_hi(nl.y)};
   const float nwh[4] = {bf16_lo(nh.x), bf16_hi(nh.x), bf16_lo(nh.y), bf16_hi(nh.y)};
   const float cosl[4] = {bf16_lo(cl.x), bf16_hi(cl.x), bf16_lo(cl.y), bf16_hi(cl.y)};
@@ -156,9 +166,8 @@ __global__ void __launch_bounds__(64) pf_qk_norm_rope_kernel(MqDecodeParams p, i
     *reinterpret_cast<uint2*>(p.kc + crow + 64 + d0) = oh;
     *reinterpret_cast<uint2*>(kt + kt_index(h, ntiles, pos, d0)) = ol;
     *reinterpret_cast<uint2*>(kt + kt_index(h, ntiles, pos, 64 + d0)) = oh;
-    const bf16_t* v = row + MQ_QDIM + MQ_KVDIM + h * MQ_D;
-    *reinterpret_cast<uint2*>(p.vc + crow + d0) = *reinterpret_cast<const uint2*>(v + d0);
-    *reinterpret_cast<uint2*>(p.vc + crow + 64 + d0) = *reinterpret_cast<const uint2*>(v + 64 + d0);
+    *reinterpret_cast<uint2*>(p.vc + crow + d0) = vl;
+    *reinterpret_cast<uint2*>(p.vc + crow + 64 + d0) = vh;
   }
 }
 
@@ -687,8 +696,8 @@ int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefi
     g.C = b.qkv; g.ldc = MQ_QKV; g.M = n; g.N = MQ_QKV; g.K = MQ_H;
     g.Vt = b.vt; g.vt_tiles = b.ntiles;
     gemm<EPI_STORE>(g, stream);
-    pf_qk_norm_rope_kernel<<<dim3(n, (MQ_NQ + MQ_NKV) / 4), 64, 0, stream>>>(p, l, b.qkv, b.kt,
-                                                                            b.ntiles);
+    pf_qk_norm_rope_kernel<<<dim3(n, (MQ_NQ + MQ_NKV) / 4), 64, 0, stream>>>(
+        p, l, w.q_norm, w.k_norm, b.qkv, b.kt, b.ntiles);
     pf_attn_kernel<<<dim3(MQ_NQ, (n + 31) / 32), 64 * ATT_SPLIT, 0, stream>>>(
         p, l, b.qkv, b.kt, b.vt, b.ntiles, b.att, n);
     g = GemmArgs{};
