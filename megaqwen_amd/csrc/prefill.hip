@@ -374,22 +374,35 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
     for (int nb = 0; nb < NBK; ++nb) {
       const int col = n_base + wn * WN + nb * 32 + (lane & 31);
       const int rbase = m_base + wm * WM + mb * 32;
+      // the 16 bf16 results of this lane's column, then 32-bit stores of column pairs: lanes 2c
+      // and 2c + 1 exchange their values (DPP), the even lane stores rows j < 8 of the pair and
+      // the odd lane rows j >= 8
+      uint32_t vb[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int row = rbase + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-        if (row < g.M) {
-          float v;
-          if (EPI == EPI_STORE) {
-            v = acc[0][mb][nb][j];
-          } else if (EPI == EPI_RESID) {
-            const bf16_t r = RPRE ? rres[RPRE ? mb : 0][RPRE ? nb : 0][j]
-                                  : g.R[(size_t)row * g.ldr + col];
-            v = round_bf16(acc[0][mb][nb][j]) + bf16_to_f32(r);
-          } else {
-            const float gv = round_bf16(acc[0][mb][nb][j]), uv = round_bf16(acc[NB - 1][mb][nb][j]);
-            v = silu_f(gv) * uv;
-          }
-          g.C[(size_t)row * g.ldc + col] = f32_to_bf16(v);
+        float v;
+        if (EPI == EPI_STORE) {
+          v = acc[0][mb][nb][j];
+        } else if (EPI == EPI_RESID) {
+          const bf16_t r = RPRE ? rres[RPRE ? mb : 0][RPRE ? nb : 0][j]
+                                : g.R[(size_t)min(row, g.M - 1) * g.ldr + col];
+          v = round_bf16(acc[0][mb][nb][j]) + bf16_to_f32(r);
+        } else {
+          const float gv = round_bf16(acc[0][mb][nb][j]), uv = round_bf16(acc[NB - 1][mb][nb][j]);
+          v = silu_f(gv) * uv;
+        }
+        vb[j] = f32_to_bf16(v);
+      }
+      const bool odd = lane & 1;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(
+            0, (int)vb[j], MQ_DPP_QUAD_XOR1, 0xF, 0xF, true);
+        const int row = rbase + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        if ((j < 8) != odd && row < g.M) {
+          const uint32_t pair = odd ? (other | (vb[j] << 16)) : (vb[j] | (other << 16));
+          *reinterpret_cast<uint32_t*>(g.C + (size_t)row * g.ldc + (col & ~1)) = pair;
         }
       }
       if (EPI == EPI_STORE && g.Vt != nullptr && n_base >= g.n1) {
