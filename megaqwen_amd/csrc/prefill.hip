@@ -14,10 +14,10 @@
 // then the last row's final norm (bf16) and the LM-head argmax (fused_prefill_kernels.inl:655-824).
 //
 // GEMMs are C[M,N] = A[M,K] B[N,K]^T ("NT": activations and weights both K-contiguous) on
-// v_mfma_f32_32x32x16_bf16 with fp32 accumulation: 64x64 or 32x64 workgroup tiles, K staged
-// through double-buffered LDS in steps of 64, fed by a 4-step register ring of global loads.
-// Consecutive workgroups walk N first, so with N/64 a multiple of 8 all M tiles of one weight
-// tile land on one XCD and share its L2.
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulation: 128x128, 64x64 or 32x64 workgroup tiles (by
+// M), K staged through double-buffered LDS in steps of 64 (128 for 32-row tiles), fed by a
+// register ring of global loads.  Consecutive workgroups walk N first, so with N/BN a multiple
+// of 8 all M tiles of one weight tile land on one XCD and share its L2.
 #include "mq_prefill.h"
 
 #include <math.h>
