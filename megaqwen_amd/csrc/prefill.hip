@@ -513,7 +513,9 @@ pf_attn_kernel(MqDecodeParams p, int layer, const bf16_t* __restrict__ qkv,
 #pragma unroll
     for (int s = 0; s < 8; ++s)
       sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[s]), qf[s], sacc, 0, 0, 0);
-    if (kt + 1 < t1) load_k(kt + 1);
+    // unconditional (the last tile of the range reloads itself): a conditional load here made
+    // the compiler's wait for V before the O^T MFMAs wait for these K loads as well
+    load_k(min(kt + 1, t1 - 1));
     float raw[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
