@@ -5,7 +5,7 @@
 // this path.  Per layer:
 //   xn  = bf16(RMSNorm(h) * w_in)                                   row kernel
 //   qkv = bf16(xn Wq|Wk|Wv^T)                                       MFMA GEMM  (n x 4096 x 1024)
-//   q,k = bf16(RoPE(RMSNorm_head(.) * w)); k, v -> KV cache rows    head kernel
+//   q,k = bf16(RoPE(RMSNorm_head(.) * w)); k, v -> KV cache rows    the same GEMM's epilogue
 //   att = bf16(causal GQA softmax(q k^T / sqrt(128)) v)             MFMA flash attention
 //   h   = bf16(bf16(att Wo^T) + h)                                  MFMA GEMM + residual epilogue
 //   xn  = bf16(RMSNorm(h) * w_post)
@@ -99,80 +99,8 @@ __global__ void __launch_bounds__(128) pf_rmsnorm_kernel(const bf16_t* __restric
   reinterpret_cast<uint4*>(y + (size_t)row * MQ_H)[t] = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-// Per-(position, head) q/k RMSNorm + rotate-half RoPE, rounded to bf16 in place; k and v rows go
-// to the KV cache of `layer` and k also to the attention's operand copy
-// (prefill_qk_norm_rope_kernel, fused_prefill_kernels.inl:112-258).  One wave per position and 4
-// heads of the 24 (0..15 q, 16..23 k with v): lane group g = lane / 16 takes head 4 blockIdx.y + g,
-// lane i = lane % 16 dims 4i .. 4i + 3 and their RoPE partners 64 + 4i .. 64 + 4i + 3 (8-byte
-// accesses).
-__global__ void __launch_bounds__(64) pf_qk_norm_rope_kernel(MqDecodeParams p, int layer,
-                                                             const bf16_t* __restrict__ q_norm,
-                                                             const bf16_t* __restrict__ k_norm,
-                                                             bf16_t* __restrict__ qkv,
-                                                             bf16_t* __restrict__ kt, int ntiles) {
-  const int pos = blockIdx.x, lane = threadIdx.x, i = lane & 15;
-  const int head = 4 * blockIdx.y + (lane >> 4);
-  bf16_t* row = qkv + (size_t)pos * MQ_QKV;
-  const bool is_q = head < MQ_NQ;
-  const int h = is_q ? head : head - MQ_NQ;
-  bf16_t* x = row + (is_q ? h * MQ_D : MQ_QDIM + h * MQ_D);
-  const int d0 = 4 * i;
-  // every load first (one memory round trip): the head's values, its norm weights, the RoPE row
-  // and, for k heads, the v values that go to the cache
-  const bf16_t* nw = is_q ? q_norm : k_norm;
-  const bf16_t* v = row + MQ_QDIM + MQ_KVDIM + h * MQ_D;
-  const uint2 xl = *reinterpret_cast<const uint2*>(x + d0);
-  const uint2 xh = *reinterpret_cast<const uint2*>(x + 64 + d0);
-  const uint2 nl = *reinterpret_cast<const uint2*>(nw + d0);
-  const uint2 nh = *reinterpret_cast<const uint2*>(nw + 64 + d0);
-  const uint2 cl = *reinterpret_cast<const uint2*>(p.cos + (size_t)pos * MQ_D + d0);
-  const uint2 ch = *reinterpret_cast<const uint2*>(p.cos + (size_t)pos * MQ_D + 64 + d0);
-  const uint2 sl = *reinterpret_cast<const uint2*>(p.sin + (size_t)pos * MQ_D + d0);
-  const uint2 sh = *reinterpret_cast<const uint2*>(p.sin + (size_t)pos * MQ_D + 64 + d0);
-  uint2 vl = make_uint2(0, 0), vh = make_uint2(0, 0);
-  if (!is_q) {
-    vl = *reinterpret_cast<const uint2*>(v + d0);
-    vh = *reinterpret_cast<const uint2*>(v + 64 + d0);
-  }
-  const float lo[4] = {bf16_lo(xl.x), bf16_hi(xl.x), bf16_lo(xl.y), bf16_hi(xl.y)};
-  const float hi[4] = {bf16_lo(xh.x), bf16_hi(xh.x), bf16_lo(xh.y), bf16_hi(xh.y)};
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
-  ss = row16_sum(ss);
-  const float r = rsqrtf(ss * (1.0f / MQ_D) + MQ_EPS);
-  const float nwl[4] = {bf16_lo(nl.x), bf16_hi(nl.x), bf16_lo(nl.y), bf16_hi(nl.y)};
-  const float nwh[4] = {bf16_lo(nh.x), bf16_hi(nh.x), bf16_lo(nh.y), bf16_hi(nh.y)};
-  const float cosl[4] = {bf16_lo(cl.x), bf16_hi(cl.x), bf16_lo(cl.y), bf16_hi(cl.y)};
-  const float cosh_[4] = {bf16_lo(ch.x), bf16_hi(ch.x), bf16_lo(ch.y), bf16_hi(ch.y)};
-  const float sinl[4] = {bf16_lo(sl.x), bf16_hi(sl.x), bf16_lo(sl.y), bf16_hi(sl.y)};
-  const float sinh_[4] = {bf16_lo(sh.x), bf16_hi(sh.x), bf16_lo(sh.y), bf16_hi(sh.y)};
-  bf16_t olo[4], ohi[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float a = lo[e] * r * nwl[e], b = hi[e] * r * nwh[e];
-    olo[e] = f32_to_bf16(a * cosl[e] - b * sinl[e]);
-    ohi[e] = f32_to_bf16(a * sinh_[e] + b * cosh_[e]);
-  }
-  const uint2 ol = make_uint2((uint32_t)olo[0] | ((uint32_t)olo[1] << 16),
-                              (uint32_t)olo[2] | ((uint32_t)olo[3] << 16));
-  const uint2 oh = make_uint2((uint32_t)ohi[0] | ((uint32_t)ohi[1] << 16),
-                              (uint32_t)ohi[2] | ((uint32_t)ohi[3] << 16));
-  *reinterpret_cast<uint2*>(x + d0) = ol;
-  *reinterpret_cast<uint2*>(x + 64 + d0) = oh;
-  if (!is_q) {
-    const size_t crow = (((size_t)layer * MQ_NKV + h) * p.max_seq + pos) * MQ_D;
-    *reinterpret_cast<uint2*>(p.kc + crow + d0) = ol;
-    *reinterpret_cast<uint2*>(p.kc + crow + 64 + d0) = oh;
-    *reinterpret_cast<uint2*>(kt + kt_index(h, ntiles, pos, d0)) = ol;
-    *reinterpret_cast<uint2*>(kt + kt_index(h, ntiles, pos, 64 + d0)) = oh;
-    *reinterpret_cast<uint2*>(p.vc + crow + d0) = vl;
-    *reinterpret_cast<uint2*>(p.vc + crow + 64 + d0) = vh;
-  }
-}
-
 // ------------------------------------------------------------------------------ GEMM
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
 
 struct GemmArgs {
   const bf16_t* A;   // [M, K]
@@ -186,8 +114,20 @@ struct GemmArgs {
   int ldc;
   const bf16_t* R;   // EPI_RESID: residual [M, N] (may alias C)
   int ldr;
-  bf16_t* Vt;        // EPI_STORE: columns [n1, N) (V) also stored as V^T operand tiles (vt_index)
-  int vt_tiles;      // 32-row tiles per kv head in Vt
+  bf16_t* Vt;        // EPI_STORE / QKV: columns [n1, N) (V) also stored as V^T operand tiles
+  int vt_tiles;      // 32-row tiles per kv head in Vt (and Kt)
+  // EPI_QKV (the q|k|v projection, N = 4096, one 128-column head per tile; rows are positions
+  // 0 .. M - 1): q/k heads get their RMSNorm (qn / kn weights) and RoPE (cs / sn tables) in the
+  // epilogue, k heads also go to the K cache (kcl, this layer's [8][max_seq][128]) and the K
+  // operand tiles (Kt, kt_index); v heads also go to the V cache (vcl)
+  const bf16_t* qn;
+  const bf16_t* kn;
+  const bf16_t* cs;
+  const bf16_t* sn;
+  bf16_t* kcl;
+  bf16_t* vcl;
+  bf16_t* Kt;
+  int max_seq;
   int M, N, K;
 };
 
@@ -205,6 +145,80 @@ struct GemmArgs {
 //   BM = 32 (BN = 64): waves 0/1 and 2/3 compute the same two 32 x 32 blocks over the first and
 //            the second half of every K step; the halves are added in LDS before the epilogue
 //            (this doubles the workgroups of the N = 1024 GEMMs at M = 512).
+// Epilogue of a q or k head tile of the q|k|v GEMM (the work of prefill_qk_norm_rope_kernel,
+// fused_prefill_kernels.inl:112-258): the bf16-rounded tile goes through LDS (row stride 136
+// bf16), then 16 threads per position take dims 4i .. 4i + 3 and their RoPE partners
+// 64 + 4i .. 64 + 4i + 3: RMSNorm over the head, weight, rotate-half RoPE, bf16; the result
+// replaces the head in C, and a k head also goes to the K cache and the K operand tiles.
+template <int BM, int BN, int MB, int NBK>
+MQ_DEV void qk_head_epilogue(const GemmArgs& g, const mq_f32x16 (&acc)[MB][NBK],
+                             unsigned char* smem, int m_base, int n_base, int row0, int col0) {
+  constexpr int TS = BN + 8;
+  bf16_t* T = reinterpret_cast<bf16_t*>(smem);
+  static_assert(TS <= 2 * (GEMM_BK + 8), "the tile fits the A staging buffers (2 x BM rows)");
+  const int t = threadIdx.x, lane = t & 63;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = row0 + mb * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        T[r * TS + col0 + nb * 32 + (lane & 31)] = f32_to_bf16(acc[mb][nb][j]);
+      }
+  __syncthreads();
+  const bool is_q = n_base < g.n0;
+  const int h = (is_q ? n_base : n_base - g.n0) >> 7;
+  const int i = t & 15, d0 = 4 * i;
+  const bf16_t* nw = is_q ? g.qn : g.kn;
+  const uint2 nl = *reinterpret_cast<const uint2*>(nw + d0);
+  const uint2 nh = *reinterpret_cast<const uint2*>(nw + 64 + d0);
+  const float nwl[4] = {bf16_lo(nl.x), bf16_hi(nl.x), bf16_lo(nl.y), bf16_hi(nl.y)};
+  const float nwh[4] = {bf16_lo(nh.x), bf16_hi(nh.x), bf16_lo(nh.y), bf16_hi(nh.y)};
+  for (int r = t >> 4; r < BM; r += 16) {
+    const int pos = m_base + r;
+    if (pos >= g.M) break;     // whole 16-lane groups leave together
+    const uint2 xl = *reinterpret_cast<const uint2*>(T + r * TS + d0);
+    const uint2 xh = *reinterpret_cast<const uint2*>(T + r * TS + 64 + d0);
+    const uint2 cl = *reinterpret_cast<const uint2*>(g.cs + (size_t)pos * MQ_D + d0);
+    const uint2 ch = *reinterpret_cast<const uint2*>(g.cs + (size_t)pos * MQ_D + 64 + d0);
+    const uint2 sl = *reinterpret_cast<const uint2*>(g.sn + (size_t)pos * MQ_D + d0);
+    const uint2 sh = *reinterpret_cast<const uint2*>(g.sn + (size_t)pos * MQ_D + 64 + d0);
+    const float lo[4] = {bf16_lo(xl.x), bf16_hi(xl.x), bf16_lo(xl.y), bf16_hi(xl.y)};
+    const float hi[4] = {bf16_lo(xh.x), bf16_hi(xh.x), bf16_lo(xh.y), bf16_hi(xh.y)};
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
+    ss = row16_sum(ss);
+    const float rs = rsqrtf(ss * (1.0f / MQ_D) + MQ_EPS);
+    const float cosl[4] = {bf16_lo(cl.x), bf16_hi(cl.x), bf16_lo(cl.y), bf16_hi(cl.y)};
+    const float cosh_[4] = {bf16_lo(ch.x), bf16_hi(ch.x), bf16_lo(ch.y), bf16_hi(ch.y)};
+    const float sinl[4] = {bf16_lo(sl.x), bf16_hi(sl.x), bf16_lo(sl.y), bf16_hi(sl.y)};
+    const float sinh_[4] = {bf16_lo(sh.x), bf16_hi(sh.x), bf16_lo(sh.y), bf16_hi(sh.y)};
+    bf16_t olo[4], ohi[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = lo[e] * rs * nwl[e], b = hi[e] * rs * nwh[e];
+      olo[e] = f32_to_bf16(a * cosl[e] - b * sinl[e]);
+      ohi[e] = f32_to_bf16(a * sinh_[e] + b * cosh_[e]);
+    }
+    const uint2 ol = make_uint2((uint32_t)olo[0] | ((uint32_t)olo[1] << 16),
+                                (uint32_t)olo[2] | ((uint32_t)olo[3] << 16));
+    const uint2 oh = make_uint2((uint32_t)ohi[0] | ((uint32_t)ohi[1] << 16),
+                                (uint32_t)ohi[2] | ((uint32_t)ohi[3] << 16));
+    bf16_t* x = g.C + (size_t)pos * g.ldc + n_base;
+    *reinterpret_cast<uint2*>(x + d0) = ol;
+    *reinterpret_cast<uint2*>(x + 64 + d0) = oh;
+    if (!is_q) {
+      bf16_t* kr = g.kcl + ((size_t)h * g.max_seq + pos) * MQ_D;
+      *reinterpret_cast<uint2*>(kr + d0) = ol;
+      *reinterpret_cast<uint2*>(kr + 64 + d0) = oh;
+      *reinterpret_cast<uint2*>(g.Kt + kt_index(h, g.vt_tiles, pos, d0)) = ol;
+      *reinterpret_cast<uint2*>(g.Kt + kt_index(h, g.vt_tiles, pos, 64 + d0)) = oh;
+    }
+  }
+}
+
 template <int EPI, int BM, int BN>
 __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
   constexpr int NB = EPI == EPI_SWIGLU ? 2 : 1;   // weight tiles per step (gate and up)
@@ -366,6 +380,15 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
     for (int j = 0; j < 16; ++j) acc[0][0][0][j] += red[(wn * 16 + j) * 64 + lane];
   }
 
+  if constexpr (EPI == EPI_QKV) {
+    static_assert(BN == 128 && KG == 1, "one head per tile");
+    if (n_base < g.n1) {
+      qk_head_epilogue<BM, BN, MB, NBK>(g, acc[0], reinterpret_cast<unsigned char*>(&As[0][0]),
+                                        m_base, n_base, wm * WM, wn * WN);
+      return;
+    }
+  }
+
   // epilogue: acc[.][mb][nb][j] is C[row][col] with row = 32 mb + 8 (j / 4) + 4 (lane / 32) +
   // j % 4, col = 32 nb + lane % 32 within the wave's tile
 #pragma unroll
@@ -382,7 +405,7 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
       for (int j = 0; j < 16; ++j) {
         const int row = rbase + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
         float v;
-        if (EPI == EPI_STORE) {
+        if (EPI == EPI_STORE || EPI == EPI_QKV) {
           v = acc[0][mb][nb][j];
         } else if (EPI == EPI_RESID) {
           const bf16_t r = RPRE ? rres[RPRE ? mb : 0][RPRE ? nb : 0][j]
@@ -403,9 +426,15 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
         if ((j < 8) != odd && row < g.M) {
           const uint32_t pair = odd ? (other | (vb[j] << 16)) : (vb[j] | (other << 16));
           *reinterpret_cast<uint32_t*>(g.C + (size_t)row * g.ldc + (col & ~1)) = pair;
+          if (EPI == EPI_QKV) {
+            // v heads (the q/k tiles returned before the loop): the V cache row too
+            const int d = (col & ~1) - g.n1;
+            *reinterpret_cast<uint32_t*>(
+                g.vcl + ((size_t)(d >> 7) * g.max_seq + row) * MQ_D + (d & 127)) = pair;
+          }
         }
       }
-      if (EPI == EPI_STORE && g.Vt != nullptr && n_base >= g.n1) {
+      if ((EPI == EPI_STORE || EPI == EPI_QKV) && g.Vt != nullptr && n_base >= g.n1) {
         // V^T operand tiles: accumulator elements 4 jg .. 4 jg + 3 are 4 consecutive keys (rows),
         // which are 4 consecutive bf16 of one V^T lane slot
         const int d = col - g.n1, h = d >> 7, dd = d & 127;
@@ -681,6 +710,13 @@ static void gemm(const GemmArgs& g, hipStream_t s) {
       pf_gemm_kernel<EPI, 128, 64><<<dim3(g.N / 64, mt128), 256, 0, s>>>(g);
       return;
     }
+  } else if constexpr (EPI == EPI_QKV) {
+    // one 128-column head per tile
+    if ((g.N / 128) * mt128 >= 512)
+      pf_gemm_kernel<EPI, 128, 128><<<dim3(g.N / 128, mt128), 256, 0, s>>>(g);
+    else
+      pf_gemm_kernel<EPI, 64, 128><<<dim3(g.N / 128, (g.M + 63) / 64), 256, 0, s>>>(g);
+    return;
   } else {
     if ((g.N / 128) * mt128 >= 512) {
       pf_gemm_kernel<EPI, 128, 128><<<dim3(g.N / 128, mt128), 256, 0, s>>>(g);
@@ -691,7 +727,8 @@ static void gemm(const GemmArgs& g, hipStream_t s) {
       return;
     }
   }
-  pf_gemm_kernel<EPI, 64, 64><<<dim3(g.N / 64, (g.M + 63) / 64), 256, 0, s>>>(g);
+  if constexpr (EPI != EPI_QKV)
+    pf_gemm_kernel<EPI, 64, 64><<<dim3(g.N / 64, (g.M + 63) / 64), 256, 0, s>>>(g);
 }
 
 int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefillBuffers& b,
@@ -710,9 +747,11 @@ int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefi
     g.B0 = w.wq; g.B1 = w.wk; g.B2 = w.wv; g.n0 = MQ_QDIM; g.n1 = MQ_QDIM + MQ_KVDIM;
     g.C = b.qkv; g.ldc = MQ_QKV; g.M = n; g.N = MQ_QKV; g.K = MQ_H;
     g.Vt = b.vt; g.vt_tiles = b.ntiles;
-    gemm<EPI_STORE>(g, stream);
-    pf_qk_norm_rope_kernel<<<dim3(n, (MQ_NQ + MQ_NKV) / 4), 64, 0, stream>>>(
-        p, l, w.q_norm, w.k_norm, b.qkv, b.kt, b.ntiles);
+    g.qn = w.q_norm; g.kn = w.k_norm; g.cs = p.cos; g.sn = p.sin; g.max_seq = p.max_seq;
+    g.kcl = p.kc + (size_t)l * MQ_NKV * p.max_seq * MQ_D;
+    g.vcl = p.vc + (size_t)l * MQ_NKV * p.max_seq * MQ_D;
+    g.Kt = b.kt;
+    gemm<EPI_QKV>(g, stream);
     pf_attn_kernel<<<dim3(MQ_NQ, (n + 31) / 32), 64 * ATT_SPLIT, 0, stream>>>(
         p, l, b.qkv, b.kt, b.vt, b.ntiles, b.att, n);
     g = GemmArgs{};
