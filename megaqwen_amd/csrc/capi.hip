@@ -7,6 +7,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <new>
@@ -49,6 +50,17 @@ Layout layout_of(const mq_model_desc* d) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Integer tuning knob from the environment (the reference reads its kernel switches the same
+// way, e.g. MEGAQWEN_FUSE_LM_HEAD); out-of-range or malformed values fall back to `dflt`.
+int env_int(const char* name, int dflt, int lo, int hi) {
+  const char* v = getenv(name);
+  if (v == nullptr || *v == 0) return dflt;
+  char* end = nullptr;
+  const long x = strtol(v, &end, 10);
+  if (end == v || *end != 0 || x < lo || x > hi) return dflt;
+  return (int)x;
+}
 
 int check_desc(const mq_model_desc* d) {
   if (d == nullptr) return fail(MQ_ERR_INVALID_ARG, "model description is NULL");
@@ -184,6 +196,7 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   p.s = reinterpret_cast<MqScratch*>(ws + lay.scratch);
   p.st = reinterpret_cast<MqState*>(ws + lay.state);
   p.scale_log2 = (float)(1.4426950408889634 / sqrt((double)MQ_D));
+  p.attn_local_max = env_int("MEGAQWEN_ATTN_LOCAL_MAX", MQ_ATT_LOCAL_DEFAULT, 0, 1 << 20);
   p.nsteps = 1;
   dec->lay = lay;
   dec->mode = mode;

@@ -799,7 +799,11 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
 //      heads) and computes its rows of the O projection restricted to the head's 256 columns.
 //   4. grid barrier; a = x + sum_h opart_h, RMSNorm, gate|up rows.
 //   5. grid barrier; down rows + a -> bf16 layer output.   6. grid barrier -> next layer.
-// That is 3 grid-wide and 2 group-local barriers per layer.
+// That is 3 grid-wide and 2 group-local barriers per layer.  For short contexts (cache length
+// <= attn_local_max) steps 2-3 collapse: every workgroup of the group attends over all
+// positions itself (its O rows prefetched with the K/V rows), and the merge barrier goes away.
+// Measured at 1 and 64 positions this wins; at 129 positions the longer attention of every
+// workgroup costs more than the barrier it saves (1404 against 1464 tok/s).
 
 // Local row i of group h's 512 q|k|v rows -> row of the fused q|k|v projection.
 MQ_DEV int grp_row(int h, int i) {
@@ -828,12 +832,26 @@ MQ_DEV void gqkv_publish(float* qkv, int h, int j, int NG, const float* lds) {
 
 // Position chunks of a group: as many chunks of at least one register slot (28 positions) as
 // the group has workgroups; chunk j = [p0, p1).  All chunks c < nch are non-empty.
+// Local mode (cache_len <= local_max): one chunk over all positions.  With `all_local` (the
+// persistent kernel) every workgroup of the group computes it, so the attention output needs no
+// exchange; otherwise (one kernel per phase) workgroup 0 of the group computes it and publishes
+// it as the only partial.  Either way the K/V cache row is written by workgroup 0 (has_pos).
 struct GAttn {
   int nch, p0, p1;
-  bool active, has_pos, small;
+  bool active, has_pos, small, local;
 };
-MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos) {
+MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos, int local_max, bool all_local) {
   GAttn g;
+  g.local = cache_len <= local_max;
+  if (g.local) {
+    g.nch = 1;
+    g.p0 = 0;
+    g.p1 = cache_len;
+    g.active = all_local || j == 0;
+    g.has_pos = j == 0;
+    g.small = cache_len <= 8;
+    return g;
+  }
   const int want = (cache_len + MQ_ATT_SLOT - 1) / MQ_ATT_SLOT;
   const int n0 = min(min(NG, MQ_MAX_CHUNKS), want);
   const int clen = (cache_len + n0 - 1) / n0;
@@ -846,6 +864,30 @@ MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos) {
   // at most two position slots (measured 1.5 against 2.0 us at 4 positions, 3.5 against 2.2 at 28)
   g.small = clen <= 8;
   return g;
+}
+// Attention output of a single chunk covering every position: o / l as the log-sum-exp merge
+// computes it for one partial (weight exp2(m - m) / l = 1 / l, then one fused multiply), so the
+// persistent kernel's local result and the one-kernel-per-phase merge of the published partial
+// are bitwise equal.
+MQ_DEV float att_single(float o, float l) { return fmaf(1.0f / l, o, 0.f); }
+// All threads, local mode: attention output of query heads 2h, 2h+1 from attn_core's LDS
+// result (ALDS_ORED, ALDS_STAT) into LDS_ATTH; ends with __syncthreads.
+MQ_DEV void attn_local_out(float* lds) {
+  const int t = tid();
+  float o = 0.f;
+  if (t < 2 * MQ_D) o = att_single(lds[ALDS_ORED + t], lds[ALDS_STAT + 2 + (t >> 7)]);
+  __syncthreads();
+  if (t < 2 * MQ_D) lds[LDS_ATTH + t] = o;
+  __syncthreads();
+}
+// Same from the single published partial of kv head h (one kernel per phase, local mode).
+MQ_DEV void group_single(const float* part, int h, float* lds) {
+  const int t = tid();
+  if (t < 2 * MQ_D) {
+    const float* src = part_ptr(const_cast<float*>(part), h, 0, t >> 7);
+    lds[LDS_ATTH + t] = att_single(ld_coh(src + 4 + (t & 127)), ld_coh(src + 1));
+  }
+  __syncthreads();
 }
 // Sync wave, after attn_core: this chunk's partial (m, l, o) of both query heads, and the new
 // position's K/V cache row from the chunk that holds it.
@@ -1128,11 +1170,11 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
   for (int step = 0; step < p.nsteps; ++step) {
     int pos, tok;
     if (!step_inputs(p, step == 0 ? p.tok_in : p.tok_out + (step - 1), pos, tok)) return;
-    const GAttn ga = gattn_plan(j, NG, pos + 1, pos);
+    const GAttn ga = gattn_plan(j, NG, pos + 1, pos, p.attn_local_max, true);
     const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
     const bf16_t* cs = p.cos + (size_t)pos * MQ_D;
     const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
-    uint32_t nbar = 0;
+    uint32_t nbar = 0, ngb = 0;
     phase_step(MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
     for (int l = 0; l < p.num_layers; ++l) {
       const MqLayerW w = lds_layer(s_layers, l);
@@ -1149,13 +1191,16 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       phase_step([&] { gqkv_publish(s->qkv, h, j, NG, lds); },
                  [&] { group_barrier_arrive(sy, h); },
                  [&] {
-                   if (!ga.active)
+                   if (!ga.active) {
                      gu_load(wgu, w, wg, G);
-                   else
+                   } else {
                      kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
                                    min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
+                     // local mode: no exchange follows the attention, so the O rows go out now
+                     if (ga.local) opart_load(wo, w, h, j, NG);
+                   }
                  },
-                 [&] { group_barrier_wait(sy, h, (uint32_t)((2 * l + 1) * NG)); },
+                 [&] { group_barrier_wait(sy, h, (++ngb) * (uint32_t)NG); },
                  [&] { if (ga.active) attn_input(s->qkv, w.q_norm, w.k_norm, cs, sn, h, lds); });
       stamp(p, wg, l, 2);
       if (ga.active) {
@@ -1164,15 +1209,23 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
         attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds, ga.small);
       }
       stamp(p, wg, l, 3);
-      phase_step([&] { if (ga.active) gattn_publish(p, l, pos, h, j, ga, lds); },
-                 [&] { group_barrier_arrive(sy, h); },
-                 [&] { opart_load(wo, w, h, j, NG); },
-                 [&] { group_barrier_wait(sy, h, (uint32_t)((2 * l + 2) * NG)); }, MQ_NOTHING);
+      if (ga.local) {
+        attn_local_out(lds);
+      } else {
+        phase_step([&] { if (ga.active) gattn_publish(p, l, pos, h, j, ga, lds); },
+                   [&] { group_barrier_arrive(sy, h); },
+                   [&] { opart_load(wo, w, h, j, NG); },
+                   [&] { group_barrier_wait(sy, h, (++ngb) * (uint32_t)NG); }, MQ_NOTHING);
+        group_merge(s->part, h, ga.nch, lds);
+      }
       stamp(p, wg, l, 4);
-      group_merge(s->part, h, ga.nch, lds);
       opart_run(wo, w, h, j, NG, lds);
       stamp(p, wg, l, 5);
-      phase_step([&] { opart_publish(&s->opart[0][0], h, j, NG, lds); },
+      phase_step([&] {
+                   opart_publish(&s->opart[0][0], h, j, NG, lds);
+                   // local mode: the new position's K/V row (ALDS_KN/VN are still intact)
+                   if (ga.local && ga.has_pos) attn_cache_row(p, l, h, pos, lds);
+                 },
                  [&] { grid_barrier_arrive(sy); },
                  [&] { if (ga.active) gu_load(wgu, w, wg, G); },
                  [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); }, MQ_NOTHING);
@@ -1244,7 +1297,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       phase_finish([&] { gqkv_publish(s->qkv, h, j, NG, lds); });
     }
     if constexpr (PH == 1) {
-      const GAttn ga = gattn_plan(j, NG, pos + 1, pos);
+      const GAttn ga = gattn_plan(j, NG, pos + 1, pos, p.attn_local_max, false);
       if (ga.active) {
         KvBlock kv;
         kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
@@ -1260,10 +1313,13 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       }
     }
     if constexpr (PH == 2) {
-      const GAttn ga = gattn_plan(j, NG, pos + 1, pos);
+      const GAttn ga = gattn_plan(j, NG, pos + 1, pos, p.attn_local_max, false);
       OPairSet ws;
       opart_load(ws, w, h, j, NG);
-      group_merge(s->part, h, ga.nch, lds);
+      if (ga.local)
+        group_single(s->part, h, lds);
+      else
+        group_merge(s->part, h, ga.nch, lds);
       opart_run(ws, w, h, j, NG, lds);
       phase_finish([&] { opart_publish(&s->opart[0][0], h, j, NG, lds); });
     }

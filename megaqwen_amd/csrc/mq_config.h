@@ -27,4 +27,5 @@
 #define MQ_ATT_NK 8                     // positions per compute-wave row per attention block
 #define MQ_ATT_BLOCK (4 * MQ_CWAVES * MQ_ATT_NK)   // 224 positions scored per pass of a chunk
 #define MQ_ATT_SLOT (4 * MQ_CWAVES)     // 28 positions: one register slot of every compute wave
+#define MQ_ATT_LOCAL_DEFAULT 64        // default attn_local_max (persistent decode)
 #define MQ_GROUPS MQ_NKV                // persistent decode: workgroup wg serves kv head wg % 8

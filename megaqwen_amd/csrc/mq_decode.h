@@ -64,6 +64,9 @@ struct MqDecodeParams {
   MqScratch* s;
   MqState* st;
   float scale_log2;            // log2(e) / sqrt(D): scores are kept in the log2 domain
+  int attn_local_max;          // cache lengths up to this are attended over all positions by
+                               // every workgroup of a kv-head group (no split-K partials, no
+                               // merge barrier); longer ones are split into position chunks
   int nsteps;                  // persistent mode: tokens decoded by one launch.  Step i reads
                                // tok_in (i = 0) or tok_out[i - 1] and writes tok_out[i]; logits
                                // are written for nsteps == 1 only

@@ -59,6 +59,25 @@ def test_decode_modes_bitwise_identical_and_deterministic(small):
     assert torch.equal(outs[0], outs[2])     # same arithmetic in both kernel organisations
 
 
+@pytest.mark.parametrize("local_max", [0, 512])
+def test_decode_attention_split_and_local(monkeypatch, local_max):
+    """Short-context attention both ways: split into position chunks with a merge barrier even at
+    the first positions (local_max 0), and computed over all positions by every workgroup of a
+    kv-head group up to position 40 (local_max 512; the default uses it below 64 positions).
+    Each against the oracle, and persistent == one-kernel-per-phase bit for bit."""
+    monkeypatch.setenv("MEGAQWEN_ATTN_LOCAL_MAX", str(local_max))
+    dec, orc, sp, _ = build_pair(2, 151936, 128, seed=2, norm_jitter=0.1)
+    toks = make_tokens(40, sp["vocab_size"], seed=7)
+    _run_teacher_forced(dec, orc, toks, "persistent")
+    outs = []
+    for mode in ("persistent", "multi_kernel"):
+        dec.set_mode(mode)
+        dec.reset()
+        outs.append(torch.stack([dec.decode_step_with_logits(int(t))[1] for t in toks]))
+    assert torch.equal(outs[0], outs[1])
+    dec.check()
+
+
 def test_decode_long_context_chunks(small):
     """Positions up to 511: several split-K chunks per kv head, merge exercised every layer."""
     dec, orc, sp, _ = small
