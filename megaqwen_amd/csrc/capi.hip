@@ -103,6 +103,7 @@ struct mq_decoder {
   int grid;
   int pos;
   int max_prefill;
+  int early_kv_mode;       // -1: long-context variant chosen by position; 0 never; 1 always
   size_t kv_bytes;
   char* ws;
   MqPrefillBuffers pf;
@@ -110,6 +111,13 @@ struct mq_decoder {
 };
 
 extern "C" {
+
+// Kernel variant of the next persistent launch (MEGAQWEN_EARLY_KV forces it either way; both
+// variants give the same results at every position).
+static int early_kv(const mq_decoder* dec) {
+  if (dec->early_kv_mode >= 0) return dec->early_kv_mode;
+  return mq_decode_early_kv(dec->pos, dec->grid, dec->p.attn_local_max);
+}
 
 int mq_abi_version(void) { return MQ_ABI_VERSION; }
 
@@ -197,7 +205,9 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   p.st = reinterpret_cast<MqState*>(ws + lay.state);
   p.scale_log2 = (float)(1.4426950408889634 / sqrt((double)MQ_D));
   p.attn_local_max = env_int("MEGAQWEN_ATTN_LOCAL_MAX", MQ_ATT_LOCAL_DEFAULT, 0, 1 << 20);
+  p.early_kv = 0;
   p.nsteps = 1;
+  dec->early_kv_mode = env_int("MEGAQWEN_EARLY_KV", -1, -1, 1);
   dec->lay = lay;
   dec->mode = mode;
   dec->grid = grid;
@@ -272,6 +282,7 @@ int mq_decode_step(mq_decoder* dec, const int32_t* d_token_in, int32_t* d_token_
     return fail(MQ_ERR_POSITION, "decode position %d reaches max_seq_len %d", dec->pos,
                 dec->p.max_seq);
   MqDecodeParams p = dec->p;
+  p.early_kv = early_kv(dec);
   p.tok_in = d_token_in;
   p.tok_out = d_token_out;
   p.logits = d_logits;
@@ -291,6 +302,7 @@ int mq_debug_decode_step_layers(mq_decoder* dec, const int32_t* d_token_in,
     return fail(MQ_ERR_POSITION, "decode position %d reaches max_seq_len %d", dec->pos,
                 dec->p.max_seq);
   MqDecodeParams p = dec->p;
+  p.early_kv = early_kv(dec);
   p.tok_in = d_token_in;
   p.tok_out = d_token_out;
   p.logits = d_logits;
@@ -311,6 +323,7 @@ int mq_debug_decode_step_timing(mq_decoder* dec, const int32_t* d_token_in,
     return fail(MQ_ERR_POSITION, "decode position %d reaches max_seq_len %d", dec->pos,
                 dec->p.max_seq);
   MqDecodeParams p = dec->p;
+  p.early_kv = early_kv(dec);
   p.tok_in = d_token_in;
   p.tok_out = d_token_out;
   p.stamps = d_stamps;
@@ -331,6 +344,7 @@ int mq_decode_steps(mq_decoder* dec, int32_t* d_tokens, int n, void* stream) {
   const int per = dec->mode == MQ_MODE_PERSISTENT ? MQ_STEPS_PER_LAUNCH : 1;
   for (int i = 0; i < n; i += per) {
     MqDecodeParams p = dec->p;
+    p.early_kv = early_kv(dec);
     p.nsteps = n - i < per ? n - i : per;
     p.tok_in = d_tokens + i;
     p.tok_out = d_tokens + i + 1;

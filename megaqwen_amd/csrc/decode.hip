@@ -29,6 +29,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 // Thread index hidden behind an empty asm so that per-lane address arithmetic is recomputed in
 // every phase instead of being hoisted out of the 28-layer loop of the persistent kernel (where
 // it would pin ~60 VGPRs for the whole kernel).
@@ -361,6 +363,22 @@ MQ_DEV void kv_block_load(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int bl
     } else {
       b.k[k] = b.v[k] = make_uint4(0, 0, 0, 0);
     }
+  }
+}
+// Same block with a fixed instruction count: every compute wave issues all 2 * MQ_ATT_NK loads,
+// positions past bend re-reading row blk (a written row; attn_core masks those lanes).  Used for
+// the early prefetch of long contexts, where the compiler must know how many loads follow the
+// q|k|v weights to wait for those alone.
+template <bool K, bool V>
+MQ_DEV void kv_block_load_all(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int blk, int bend) {
+  const int lane = lane_id(), wave = wave_id();
+  if (wave >= MQ_CWAVES) return;
+#pragma unroll
+  for (int k = 0; k < MQ_ATT_NK; ++k) {
+    const int pp = blk + k * 4 * MQ_CWAVES + wave * 4 + (lane >> 4);
+    const size_t off = (size_t)(pp < bend ? pp : blk) * MQ_D;
+    if constexpr (K) b.k[k] = ld16(Kb + off);
+    if constexpr (V) b.v[k] = ld16(Vb + off);
   }
 }
 MQ_DEV const bf16_t* kv_base(const bf16_t* cache, const MqDecodeParams& p, int layer, int h) {
@@ -1142,6 +1160,14 @@ MQ_DEV void step_wait(const MqDecodeParams& p, uint32_t target) {
   __syncthreads();
 }
 
+// EARLY: the long-context variant (chosen per launch by the host, MqDecodeParams.early_kv): a
+// layer's K rows are issued right after its q|k|v weights, one phase earlier than otherwise, so
+// they stream in during the q|k|v dot products and the group barrier; its V rows follow at the
+// q|k|v barrier.  Both K/V loads have a fixed instruction count (kv_block_load_all), so the
+// compiler waits for the q|k|v weights alone.  The variant is correct at any position: steps
+// where a workgroup has no chunk load row 0 and ignore it, and chunks of <= 8 positions use the
+// 7-wave layout.  (One kernel holding both variants spilled ~600 VGPRs.)
+template <bool EARLY>
 __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDecodeParams p) {
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   __shared__ MqLayerW s_layers[MQ_MAX_LAYERS];
@@ -1176,6 +1202,16 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
     uint32_t nbar = 0, ngb = 0;
     phase_step(MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
+    // K/V block of this workgroup's chunk (EARLY: row 0 for a workgroup without one)
+    const bool small = EARLY ? false : ga.small;
+    const int kv0 = ga.active ? ga.p0 : 0;
+    const int kv1 = ga.active ? min(ga.p1, ga.p0 + MQ_ATT_BLOCK) : 1;
+    auto k_early = [&](int l) {
+      kv_block_load_all<true, false>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), kv0, kv1);
+    };
+    if constexpr (EARLY) {
+      if (p.num_layers > 0) k_early(0);
+    }
     for (int l = 0; l < p.num_layers; ++l) {
       const MqLayerW w = lds_layer(s_layers, l);
       stamp(p, wg, l, 0);
@@ -1191,13 +1227,19 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       phase_step([&] { gqkv_publish(s->qkv, h, j, NG, lds); },
                  [&] { group_barrier_arrive(sy, h); },
                  [&] {
-                   if (!ga.active) {
-                     gu_load(wgu, w, wg, G);
-                   } else {
-                     kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
-                                   min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
-                     // local mode: no exchange follows the attention, so the O rows go out now
+                   if constexpr (EARLY) {
+                     kv_block_load_all<false, true>(kv, kv_base(p.kc, p, l, h),
+                                                    kv_base(p.vc, p, l, h), kv0, kv1);
                      if (ga.local) opart_load(wo, w, h, j, NG);
+                   } else {
+                     if (!ga.active) {
+                       gu_load(wgu, w, wg, G);
+                     } else {
+                       kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
+                                     min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
+                       // local mode: no exchange follows the attention, so the O rows go now
+                       if (ga.local) opart_load(wo, w, h, j, NG);
+                     }
                    }
                  },
                  [&] { group_barrier_wait(sy, h, (++ngb) * (uint32_t)NG); },
@@ -1206,7 +1248,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       if (ga.active) {
         attn_prologue(lds);
         __syncthreads();
-        attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds, ga.small);
+        attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds, small);
       }
       stamp(p, wg, l, 3);
       if (ga.local) {
@@ -1247,7 +1289,12 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
             down_publish(wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); });
           },
           [&] { grid_barrier_arrive(sy); },
-          [&] { if (l + 1 < p.num_layers) gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG); },
+          [&] {
+            if (l + 1 < p.num_layers) {
+              gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG);
+              if constexpr (EARLY) k_early(l + 1);
+            }
+          },
           [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); },
           [&] { input_hidden_coh(lds, s->hidden); });
       stamp(p, wg, l, 10);
@@ -1486,7 +1533,7 @@ static int device_info() {
     coop = 0;
   int nb = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &nb, reinterpret_cast<const void*>(mq_decode_persistent_kernel), MQ_THREADS, 0) !=
+          &nb, reinterpret_cast<const void*>(mq_decode_persistent_kernel<false>), MQ_THREADS, 0) !=
       hipSuccess)
     nb = 0;
   g_cu_count = cu;
@@ -1515,9 +1562,9 @@ int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t st
   if (mode == MQ_MODE_PERSISTENT) {
     MqDecodeParams pc = p;
     void* args[] = {&pc};
-    hipError_t e = hipLaunchCooperativeKernel(
-        reinterpret_cast<const void*>(mq_decode_persistent_kernel), dim3(grid), dim3(MQ_THREADS),
-        args, 0, stream);
+    const void* fn = p.early_kv ? reinterpret_cast<const void*>(mq_decode_persistent_kernel<true>)
+                                : reinterpret_cast<const void*>(mq_decode_persistent_kernel<false>);
+    hipError_t e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(MQ_THREADS), args, 0, stream);
     return e == hipSuccess ? 0 : -(int)e - 1000;
   }
   for (int l = 0; l < p.num_layers; ++l) {

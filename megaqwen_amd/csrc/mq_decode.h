@@ -67,6 +67,9 @@ struct MqDecodeParams {
   int attn_local_max;          // cache lengths up to this are attended over all positions by
                                // every workgroup of a kv-head group (no split-K partials, no
                                // merge barrier); longer ones are split into position chunks
+  int early_kv;                // persistent mode: launch the long-context variant that issues
+                               // each layer's K rows with its q|k|v weights (host-chosen per
+                               // launch, mq_decode_early_kv; correct at any position)
   int nsteps;                  // persistent mode: tokens decoded by one launch.  Step i reads
                                // tok_in (i = 0) or tok_out[i - 1] and writes tok_out[i]; logits
                                // are written for nsteps == 1 only
@@ -102,6 +105,13 @@ __host__ __device__ inline int mq_attn_chunk_len(int cache_len, int nch) {
 #endif
 
 int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t stream);
+// Whether a persistent launch starting at `pos` should use the long-context variant: every
+// workgroup of a group then holds an attention chunk in every step of the launch (positions
+// only grow within a launch), and the short-context local mode no longer applies.
+__host__ __device__ inline int mq_decode_early_kv(int pos, int grid, int local_max) {
+  const int cache_len = pos + 1;
+  return cache_len >= (grid / MQ_GROUPS) * MQ_ATT_SLOT && cache_len > local_max ? 1 : 0;
+}
 int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream);
 int mq_launch_zero(void* ptr, size_t bytes, hipStream_t stream);
 int mq_decode_grid(int mode, int* grid_out);

@@ -78,6 +78,40 @@ def test_decode_attention_split_and_local(monkeypatch, local_max):
     dec.check()
 
 
+def test_decode_early_kv_variant(monkeypatch):
+    """The long-context kernel variant (K rows issued with the q|k|v weights) is correct at any
+    position: forced from the first step it matches the oracle, and it equals the other variant
+    bit for bit wherever both use the same chunk layout (chunks above 8 positions), also after a
+    1000-token prefill, where the position-based choice picks it."""
+    decs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("MEGAQWEN_EARLY_KV", mode)
+        decs[mode] = build_pair(2, 151936, 1100, seed=2, norm_jitter=0.1, max_prefill=1024,
+                                oracle=mode == "1")
+    dec1, orc, sp, _ = decs["1"]
+    dec0 = decs["0"][0]
+    toks = make_tokens(40, sp["vocab_size"], seed=8)
+    _run_teacher_forced(dec1, orc, toks, "persistent")
+    # from position 9 on (a prefill writes the first rows the same way for both), the short
+    # chunks are above 8 positions, so both variants run the same arithmetic
+    outs = []
+    for dec in (dec1, dec0):
+        dec.set_mode("persistent")
+        dec.reset()
+        dec.prefill_step(make_tokens(9, sp["vocab_size"], seed=10).to(torch.int32))
+        outs.append(torch.stack([dec.decode_step_with_logits(int(t))[1] for t in toks]))
+    assert torch.equal(outs[0], outs[1])
+    prompt = make_tokens(1000, sp["vocab_size"], seed=9)
+    longs = []
+    for dec in (dec1, dec0):
+        dec.reset()
+        t = dec.prefill_step(prompt.to(torch.int32))
+        longs.append(torch.stack([dec.decode_step_with_logits(int(u))[1]
+                                  for u in [t] + toks[:4].tolist()]))
+        dec.check()
+    assert torch.equal(longs[0], longs[1])
+
+
 def test_decode_long_context_chunks(small):
     """Positions up to 511: several split-K chunks per kv head, merge exercised every layer."""
     dec, orc, sp, _ = small
