@@ -283,6 +283,11 @@ MQ_DEV void grid_barrier_wait(MqSync* s, uint32_t target) {
     const uint32_t e = __builtin_amdgcn_readlane(v, 63);
     const uint32_t total = __builtin_amdgcn_readfirstlane(row16_sum_u32(v));
     if (e != 0 || (int32_t)(total - target) >= 0) break;
+    // back-off of ~128 clocks between polls: 256 workgroups x 16 lanes polling the stripe lines
+    // back to back slow down the arrivals on those lines (measured 1496-1508 against 1440 tok/s
+    // at pos 128 on one box; 1 to 8 units of s_sleep measure alike, the group barrier's single
+    // poller gains nothing from it)
+    __builtin_amdgcn_s_sleep(2);
     if (++spins > MQ_SPIN_LIMIT) {
       if (lane == 0)
         __hip_atomic_store(&s->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
