@@ -1150,6 +1150,7 @@ MQ_DEV void step_wait(const MqDecodeParams& p, uint32_t target) {
       const uint32_t e = __builtin_amdgcn_readlane(v, 63);
       const uint32_t c = __builtin_amdgcn_readlane(v, 0);
       if (e != 0 || (int32_t)(c - target) >= 0) break;
+      __builtin_amdgcn_s_sleep(2);   // back-off, as in the grid barrier
       if (++spins > MQ_SPIN_LIMIT) {
         if (lane == 0)
           __hip_atomic_store(&p.st->sync.err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

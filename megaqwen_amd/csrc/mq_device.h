@@ -277,9 +277,10 @@ MQ_DEV void grid_barrier_wait(MqSync* s, uint32_t target) {
   uint32_t spins = 0;
   while (true) {
     uint32_t v = 0;
+    // the error flag (one line that every workgroup would poll) is read on every 8th poll only
     if (lane < MQ_BAR_STRIPES)
       v = __hip_atomic_load(&s->bar[lane].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else if (lane == 63)
+    else if (lane == 63 && (spins & 7) == 0)
       v = __hip_atomic_load(&s->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t e = __builtin_amdgcn_readlane(v, 63);
     const uint32_t rs = row16_sum_u32(v);
