@@ -100,7 +100,8 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
                       size_t workspace_bytes, mq_decoder** out);
 int mq_decoder_destroy(mq_decoder* dec);
 
-/* reset(): zeroes both KV caches and sets the position to 0 (bindings_decode.cpp:236-240). */
+/* reset(): zeroes both KV caches and sets the position to 0 (bindings_decode.cpp:236-240); also
+ * clears the device error flag (see mq_decoder_check). */
 int mq_decoder_reset(mq_decoder* dec, void* stream);
 /* position() (bindings_decode.cpp:273-280).  Returns the host-side position counter. */
 int mq_decoder_position(const mq_decoder* dec);
@@ -148,13 +149,17 @@ int mq_debug_decode_step_layers(mq_decoder* dec, const int32_t* d_token_in,
 int mq_debug_decode_step_timing(mq_decoder* dec, const int32_t* d_token_in,
                                 int32_t* d_token_out, uint64_t* d_stamps, void* stream);
 
-/* Synchronises `stream` and returns MQ_ERR_DEVICE if a kernel flagged an error. */
+/* Synchronises `stream` and returns MQ_ERR_DEVICE if a kernel flagged an error (barrier time-out,
+ * bad position or token id).  The flag stays set until mq_decoder_reset; while it is set the
+ * decode kernels skip their barrier waits, so results are not meaningful. */
 int mq_decoder_check(mq_decoder* dec, void* stream);
 
 /* prefill_step (bindings_prefill.cpp:731-833) over launch_prefill_float
  * (fused_prefill_launch.inl:71-731): runs tokens d_tokens[0..n) at positions 0..n-1, fills the
  * KV cache, writes the greedy next token to d_token_out (and the last position's fp32 logits to
- * d_logits if non-NULL) and sets the position to n.  1 <= n <= max_prefill_len. */
+ * d_logits if non-NULL) and sets the position to n.  1 <= n <= max_prefill_len.  A token id
+ * outside [0, vocab_size) is read as id 0 and sets the device error flag that
+ * mq_decoder_check reports (the ids stay on the device, so they are not checked on the host). */
 int mq_prefill(mq_decoder* dec, const int32_t* d_tokens, int n, int32_t* d_token_out,
                float* d_logits, void* stream);
 
@@ -167,6 +172,12 @@ int mq_prefill(mq_decoder* dec, const int32_t* d_tokens, int n, int32_t* d_token
 int mq_prefill_embeds(mq_decoder* dec, const int32_t* d_tokens, int n, const void* d_embeds,
                       int embeds_start, int embeds_len, int32_t* d_token_out, float* d_logits,
                       void* stream);
+
+/* Debug hook: mq_prefill that also writes the residual stream after every layer to d_trace
+ * (bf16 [num_layers][n][hidden_size]), for layer-by-layer parity checks of the prefill path
+ * (launch_prefill_float's per-layer hidden_bf16, fused_prefill_launch.inl:245-657). */
+int mq_debug_prefill_layers(mq_decoder* dec, const int32_t* d_tokens, int n,
+                            int32_t* d_token_out, float* d_logits, void* d_trace, void* stream);
 
 /* Debug hook: device addresses (inside the workspace) of the prefill buffers of the last
  * prefill: out5 = {h [n,H], xn [n,H], qkv [n,Hq*D+2*Hkv*D], att [n,Hq*D], mlp [n,I]}, bf16. */

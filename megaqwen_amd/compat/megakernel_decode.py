@@ -27,7 +27,9 @@ if _ROOT not in sys.path:
     sys.path.insert(0, _ROOT)
 
 from megaqwen_amd import spec as _spec  # noqa: E402
-from megaqwen_amd.decoder import MegakernelDecoder, MegakernelPrefillDecoder  # noqa: E402
+from megaqwen_amd.decoder import (  # noqa: E402
+    MegakernelDecoder, MegakernelFusedPrefillDecoder, MegakernelPrefillDecoder,
+)
 from megaqwen_amd.generators import (  # noqa: E402
     MegakernelFusedPrefillGenerator, MegakernelGenerator, MegakernelPrefillGenerator,
 )
@@ -69,7 +71,7 @@ def _compile_prefill_kernel():
 
 
 def _compile_fused_prefill_kernel():
-    return types.SimpleNamespace(MegakernelFusedPrefillDecoder=MegakernelPrefillDecoder)
+    return types.SimpleNamespace(MegakernelFusedPrefillDecoder=MegakernelFusedPrefillDecoder)
 
 
 _refresh_spec_aliases()

@@ -216,7 +216,8 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   dec->kv_bytes = (size_t)desc->num_layers * MQ_NKV * (size_t)desc->max_seq_len * MQ_D * 2;
   dec->ws = ws;
   mq_prefill_bind(&dec->pf, ws + lay.prefill, desc->max_prefill_len);
-  if (mq_launch_fill_state(p.st, 0, nullptr) != 0 || hipStreamSynchronize(nullptr) != hipSuccess) {
+  if (mq_launch_fill_state(p.st, 0, nullptr, true) != 0 ||
+      hipStreamSynchronize(nullptr) != hipSuccess) {
     delete dec;
     return fail(MQ_ERR_HIP, "state initialisation failed");
   }
@@ -233,7 +234,8 @@ int mq_decoder_reset(mq_decoder* dec, void* stream) {
   if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "decoder is NULL");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (mq_launch_zero(dec->p.kc, dec->kv_bytes, s) != 0 ||
-      mq_launch_zero(dec->p.vc, dec->kv_bytes, s) != 0 || mq_launch_fill_state(dec->p.st, 0, s) != 0)
+      mq_launch_zero(dec->p.vc, dec->kv_bytes, s) != 0 ||
+      mq_launch_fill_state(dec->p.st, 0, s, true) != 0)
     return fail(MQ_ERR_HIP, "reset kernels failed to launch");
   dec->pos = 0;
   return MQ_OK;
@@ -396,6 +398,23 @@ int mq_prefill_embeds(mq_decoder* dec, const int32_t* d_tokens, int n, const voi
   int rc = mq_launch_prefill(dec->p, dec->host_layers.data(), dec->pf, d_tokens, n, d_token_out,
                              d_logits, dec->grid, s, static_cast<const bf16_t*>(d_embeds),
                              embeds_start, embeds_len);
+  if (rc != 0) return fail(MQ_ERR_HIP, "prefill launch failed (%d)", rc);
+  if (mq_launch_fill_state(dec->p.st, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
+  dec->pos = n;
+  return MQ_OK;
+}
+
+int mq_debug_prefill_layers(mq_decoder* dec, const int32_t* d_tokens, int n,
+                            int32_t* d_token_out, float* d_logits, void* d_trace, void* stream) {
+  if (dec == nullptr || d_tokens == nullptr || d_token_out == nullptr || d_trace == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "decoder, token and trace pointers must be non-NULL");
+  if (n <= 0) return fail(MQ_ERR_INVALID_ARG, "Empty input sequence");
+  if (n > dec->max_prefill)
+    return fail(MQ_ERR_INVALID_ARG, "Prefill sequence length %d exceeds maximum %d", n,
+                dec->max_prefill);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = mq_launch_prefill(dec->p, dec->host_layers.data(), dec->pf, d_tokens, n, d_token_out,
+                             d_logits, dec->grid, s, nullptr, 0, 0, static_cast<bf16_t*>(d_trace));
   if (rc != 0) return fail(MQ_ERR_HIP, "prefill launch failed (%d)", rc);
   if (mq_launch_fill_state(dec->p.st, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
   dec->pos = n;

@@ -345,11 +345,18 @@ MQ_DEV void attn_cache_row(const MqDecodeParams& p, int layer, int h, int pos, c
 
 // K/V of up to MQ_ATT_BLOCK positions: position blk + k*28 + wave*4 + (lane/16) goes to compute
 // wave `wave`, row lane/16, each lane holding 8 of the 128 dims (16 bytes).
+//
+// The row of the position being decoded (pos_new) is never loaded: it is written during this
+// step (attn_cache_row) and its values come from LDS instead.  Fetching it before the write would
+// leave a stale copy in this CU's L1 and this XCD's L2, and a chained launch reads the row with
+// plain loads in the next step.  Every row below pos_new was written by an earlier step (of this
+// launch, with device-scope stores ordered by the barriers in between, or of an earlier kernel)
+// and was not loaded by anyone before that write, so a plain load of it cannot hit a stale line.
 struct KvBlock {
   uint4 k[MQ_ATT_NK], v[MQ_ATT_NK];
 };
 MQ_DEV void kv_block_load(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int blk, int bend,
-                          bool small = false) {
+                          int pos_new, bool small = false) {
   const int lane = lane_id(), wave = wave_id();
   // small chunks (<= 28 positions): wave 0 holds position blk + 4k + row in slot k
   if (wave >= (small ? 1 : MQ_CWAVES)) return;
@@ -357,7 +364,7 @@ MQ_DEV void kv_block_load(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int bl
   for (int k = 0; k < MQ_ATT_NK; ++k) {
     const int pp = small ? blk + k * 4 + (lane >> 4)
                          : blk + k * 4 * MQ_CWAVES + wave * 4 + (lane >> 4);
-    if (pp < bend && (!small || k < MQ_ATT_SLOT / 4)) {
+    if (pp < bend && pp != pos_new && (!small || k < MQ_ATT_SLOT / 4)) {
       b.k[k] = ld16(Kb + (size_t)pp * MQ_D);
       b.v[k] = ld16(Vb + (size_t)pp * MQ_D);
     } else {
@@ -365,20 +372,22 @@ MQ_DEV void kv_block_load(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int bl
     }
   }
 }
-// Same block with a fixed instruction count: every compute wave issues all 2 * MQ_ATT_NK loads,
-// positions past bend re-reading row blk (a written row; attn_core masks those lanes).  Used for
-// the early prefetch of long contexts, where the compiler must know how many loads follow the
-// q|k|v weights to wait for those alone.
+// Same block with a fixed instruction count: every compute wave issues all 2 * MQ_ATT_NK loads.
+// Lanes whose position is past bend or is pos_new read the read-only row `dummy` (16 bytes per
+// lane of a 256-byte row) instead, so no unwritten cache row is fetched; attn_core masks the
+// former and replaces the latter from LDS.  Used for the early prefetch of long contexts, where
+// the compiler must know how many loads follow the q|k|v weights to wait for those alone.
 template <bool K, bool V>
-MQ_DEV void kv_block_load_all(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int blk, int bend) {
+MQ_DEV void kv_block_load_all(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int blk, int bend,
+                              int pos_new, const bf16_t* dummy) {
   const int lane = lane_id(), wave = wave_id();
   if (wave >= MQ_CWAVES) return;
 #pragma unroll
   for (int k = 0; k < MQ_ATT_NK; ++k) {
     const int pp = blk + k * 4 * MQ_CWAVES + wave * 4 + (lane >> 4);
-    const size_t off = (size_t)(pp < bend ? pp : blk) * MQ_D;
-    if constexpr (K) b.k[k] = ld16(Kb + off);
-    if constexpr (V) b.v[k] = ld16(Vb + off);
+    const bool row = pp < bend && pp != pos_new;
+    if constexpr (K) b.k[k] = ld16(row ? Kb + (size_t)pp * MQ_D : dummy);
+    if constexpr (V) b.v[k] = ld16(row ? Vb + (size_t)pp * MQ_D : dummy);
   }
 }
 MQ_DEV const bf16_t* kv_base(const bf16_t* cache, const MqDecodeParams& p, int layer, int h) {
@@ -423,7 +432,7 @@ MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1,
       // fit in registers)
       asm volatile("" ::: "memory");
       const int bend = min(p1, blk + MQ_ATT_BLOCK);
-      if (blk != p0) kv_block_load(b, Kb, Vb, blk, bend);
+      if (blk != p0) kv_block_load(b, Kb, Vb, blk, bend, pos_new);
       if (pos_new >= blk && pos_new < bend) {
         // the new position is not in the cache yet: its bf16 K/V (exact as bf16) replace the
         // registers of the lane row that holds it
@@ -1166,7 +1175,8 @@ MQ_DEV void step_wait(const MqDecodeParams& p, uint32_t target) {
 // they stream in during the q|k|v dot products and the group barrier; its V rows follow at the
 // q|k|v barrier.  Both K/V loads have a fixed instruction count (kv_block_load_all), so the
 // compiler waits for the q|k|v weights alone.  The variant is correct at any position: steps
-// where a workgroup has no chunk load row 0 and ignore it, and chunks of <= 8 positions use the
+// where a workgroup has no chunk load a stand-in K row and ignore it (and issue their gate|up
+// weights at the q|k|v boundary, as in the other variant), and chunks of <= 8 positions use the
 // 7-wave layout.  (One kernel holding both variants spilled ~600 VGPRs.)
 template <bool EARLY>
 __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDecodeParams p) {
@@ -1207,8 +1217,11 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     const bool small = EARLY ? false : ga.small;
     const int kv0 = ga.active ? ga.p0 : 0;
     const int kv1 = ga.active ? min(ga.p1, ga.p0 + MQ_ATT_BLOCK) : 1;
+    // read-only stand-in row for lanes that must not fetch a cache row (row 0 of the cos table)
+    const bf16_t* kv_dummy = p.cos + (lane_id() & 15) * 8;
     auto k_early = [&](int l) {
-      kv_block_load_all<true, false>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), kv0, kv1);
+      kv_block_load_all<true, false>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), kv0, kv1,
+                                     pos, kv_dummy);
     };
     if constexpr (EARLY) {
       if (p.num_layers > 0) k_early(0);
@@ -1229,15 +1242,22 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
                  [&] { group_barrier_arrive(sy, h); },
                  [&] {
                    if constexpr (EARLY) {
-                     kv_block_load_all<false, true>(kv, kv_base(p.kc, p, l, h),
-                                                    kv_base(p.vc, p, l, h), kv0, kv1);
-                     if (ga.local) opart_load(wo, w, h, j, NG);
+                     // a workgroup without a chunk (some cache lengths below ~990 leave the
+                     // last one idle) takes the gate|up weights here, as in the other variant
+                     if (!ga.active) {
+                       gu_load(wgu, w, wg, G);
+                     } else {
+                       kv_block_load_all<false, true>(kv, kv_base(p.kc, p, l, h),
+                                                      kv_base(p.vc, p, l, h), kv0, kv1, pos,
+                                                      kv_dummy);
+                       if (ga.local) opart_load(wo, w, h, j, NG);
+                     }
                    } else {
                      if (!ga.active) {
                        gu_load(wgu, w, wg, G);
                      } else {
                        kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
-                                     min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
+                                     min(ga.p1, ga.p0 + MQ_ATT_BLOCK), pos, ga.small);
                        // local mode: no exchange follows the attention, so the O rows go now
                        if (ga.local) opart_load(wo, w, h, j, NG);
                      }
@@ -1349,7 +1369,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       if (ga.active) {
         KvBlock kv;
         kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
-                      min(ga.p1, ga.p0 + MQ_ATT_BLOCK), ga.small);
+                      min(ga.p1, ga.p0 + MQ_ATT_BLOCK), pos, ga.small);
         phase_sync(sy, 0, false, MQ_NOTHING, [&] {
           attn_input(s->qkv, w.q_norm, w.k_norm, p.cos + (size_t)pos * MQ_D,
                      p.sin + (size_t)pos * MQ_D, h, lds);
@@ -1436,7 +1456,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_attn_kernel(MqDecodeParams p
   if (!it.active) return;
   KvBlock kv;
   kv_block_load(kv, kv_base(p.kc, p, l, it.h), kv_base(p.vc, p, l, it.h), it.p0,
-                min(it.p1, it.p0 + MQ_ATT_BLOCK));
+                min(it.p1, it.p0 + MQ_ATT_BLOCK), -1);
   if (tid() < 256) lds[ALDS_QS + tid()] = q_hat[2 * it.h * MQ_D + tid()];
   __syncthreads();
   attn_core(p, l, it.h, it.p0, it.p1, -1, kv, lds);
@@ -1500,13 +1520,13 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, 
 }
 
 // ---------------------------------------------------------------------- state kernels
-__global__ void mq_fill_state_kernel(MqState* st, int pos) {
+__global__ void mq_fill_state_kernel(MqState* st, int pos, int clear_err) {
   const int t = threadIdx.x;
   if (t < MQ_BAR_STRIPES) st->sync.bar[t].v = 0;
   if (t < MQ_NKV) st->sync.attn[t].v = 0;
   if (t == 0) {
     st->sync.done.v = 0;
-    st->sync.err.v = 0;
+    if (clear_err) st->sync.err.v = 0;
     st->sync.argmax.v = 0;
     st->pos.v = (uint32_t)pos;
     st->steps.v = 0;
@@ -1579,8 +1599,8 @@ int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t st
   return launch_status();
 }
 
-int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream) {
-  mq_fill_state_kernel<<<1, 64, 0, stream>>>(st, pos);
+int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream, bool clear_err) {
+  mq_fill_state_kernel<<<1, 64, 0, stream>>>(st, pos, clear_err ? 1 : 0);
   return launch_status();
 }
 

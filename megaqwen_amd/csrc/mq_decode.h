@@ -112,7 +112,10 @@ __host__ __device__ inline int mq_decode_early_kv(int pos, int grid, int local_m
   const int cache_len = pos + 1;
   return cache_len >= (grid / MQ_GROUPS) * MQ_ATT_SLOT && cache_len > local_max ? 1 : 0;
 }
-int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream);
+// Clears the barrier / completion state and sets the device position; the error flag is kept
+// (sticky until mq_decoder_reset or creation, so mq_decoder_check still reports it) unless
+// `clear_err`.
+int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream, bool clear_err = false);
 int mq_launch_zero(void* ptr, size_t bytes, hipStream_t stream);
 int mq_decode_grid(int mode, int* grid_out);
 int mq_read_error(MqState* st, hipStream_t stream, uint32_t* err_out);

@@ -20,7 +20,8 @@ void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n);
 // `host_layers` is the host copy of the device layer table p.layers.
 // `patch` (optional, bf16 [patch_len, H]) replaces the embedding rows
 // [patch_start, patch_start + patch_len), which must lie inside [0, n).
+// `trace` (optional, bf16 [num_layers][n][H]) receives the residual stream after every layer.
 int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* host_layers,
                       const MqPrefillBuffers& b, const int32_t* tokens, int n, int32_t* tok_out,
                       float* logits, int grid, hipStream_t stream, const bf16_t* patch = nullptr,
-                      int patch_start = 0, int patch_len = 0);
+                      int patch_start = 0, int patch_len = 0, bf16_t* trace = nullptr);

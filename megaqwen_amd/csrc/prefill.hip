@@ -58,15 +58,24 @@ MQ_DEV size_t vt_index(int h, int ntiles, int key, int d) {
 // Embedding gather (prefill_embed_kernel, fused_prefill_kernels.inl:3-20); rows
 // [patch_start, patch_start + patch_len) take the caller's bf16 rows instead (the audio span of
 // prefill_patch_audio_kernel, fused_prefill_kernels.inl:28-45, fused into the gather).
+// A token id outside [0, vocab) reads row 0 instead and sets the error flag to 2 (as the decode
+// kernels do for their input token), so a bad id never reads outside the embedding table.
 __global__ void __launch_bounds__(128) pf_embed_kernel(const bf16_t* __restrict__ embed,
                                                        const int32_t* __restrict__ tokens,
                                                        bf16_t* __restrict__ h,
                                                        const bf16_t* __restrict__ patch,
-                                                       int patch_start, int patch_len) {
+                                                       int patch_start, int patch_len, int vocab,
+                                                       uint32_t* err) {
   const int row = blockIdx.x;
   const int pr = row - patch_start;
-  const bf16_t* src = (pr >= 0 && pr < patch_len) ? patch + (size_t)pr * MQ_H
-                                                  : embed + (size_t)tokens[row] * MQ_H;
+  const bool patched = pr >= 0 && pr < patch_len;
+  int tok = patched ? 0 : tokens[row];
+  if (tok < 0 || tok >= vocab) {
+    if (threadIdx.x == 0)
+      __hip_atomic_store(err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    tok = 0;
+  }
+  const bf16_t* src = patched ? patch + (size_t)pr * MQ_H : embed + (size_t)tok * MQ_H;
   reinterpret_cast<uint4*>(h + (size_t)row * MQ_H)[threadIdx.x] =
       reinterpret_cast<const uint4*>(src)[threadIdx.x];
 }
@@ -733,12 +742,14 @@ static void gemm(const GemmArgs& g, hipStream_t s) {
 
 int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefillBuffers& b,
                       const int32_t* tokens, int n, int32_t* tok_out, float* logits, int grid,
-                      hipStream_t stream, const bf16_t* patch, int patch_start, int patch_len) {
+                      hipStream_t stream, const bf16_t* patch, int patch_start, int patch_len,
+                      bf16_t* trace) {
   if (n <= 0 || n > b.max_n || n > p.max_seq) return -3;
   if (patch != nullptr && (patch_len <= 0 || patch_start < 0 || patch_start + patch_len > n))
     return -3;
   if (patch == nullptr) patch_len = 0;
-  pf_embed_kernel<<<n, 128, 0, stream>>>(p.embed, tokens, b.h, patch, patch_start, patch_len);
+  pf_embed_kernel<<<n, 128, 0, stream>>>(p.embed, tokens, b.h, patch, patch_start, patch_len,
+                                         p.vocab, &p.st->sync.err.v);
   for (int l = 0; l < p.num_layers; ++l) {
     const MqLayerW& w = hl[l];
     pf_rmsnorm_kernel<<<n, 128, 0, stream>>>(b.h, w.in_ln, b.xn);
@@ -770,6 +781,10 @@ int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefi
     g.B0 = g.B1 = g.B2 = w.wd; g.n0 = g.n1 = MQ_H;
     g.C = b.h; g.ldc = MQ_H; g.R = b.h; g.ldr = MQ_H; g.M = n; g.N = MQ_H; g.K = MQ_I;
     gemm<EPI_RESID>(g, stream);
+    if (trace != nullptr &&
+        hipMemcpyAsync(trace + (size_t)l * n * MQ_H, b.h, (size_t)n * MQ_H * sizeof(bf16_t),
+                       hipMemcpyDeviceToDevice, stream) != hipSuccess)
+      return -4;
   }
   // last row: final norm rounded to bf16, LM head argmax (fused_prefill_kernels.inl:655-824)
   return mq_launch_lm_head_bf16norm(p, b.h + (size_t)(n - 1) * MQ_H, tok_out, logits, grid,

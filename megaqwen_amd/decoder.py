@@ -33,6 +33,15 @@ def _stream_ptr() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+class _PrefillLimit(int):
+    """An int that can also be called: `dec.max_prefill_len` reads it as an attribute and
+    `dec.max_prefill_len()` as the method of the reference's fused-prefill decoder
+    (bindings_fused_prefill.cpp:536)."""
+
+    def __call__(self) -> int:
+        return int(self)
+
+
 def _bf16_cuda(t: torch.Tensor, name: str) -> torch.Tensor:
     if not isinstance(t, torch.Tensor) or not t.is_cuda:
         raise TypeError(f"{name} must be a CUDA tensor")
@@ -63,7 +72,7 @@ class MegakernelDecoder:
             raise ValueError("RoPE tables must cover max_seq_len positions")
         self.num_layers = num_layers
         self.max_seq_len = max_seq_len
-        self.max_prefill_len = int(max_prefill_len)
+        self.max_prefill_len = _PrefillLimit(int(max_prefill_len))
         self.vocab_size = int(vocab)
         device = self.embed_weight.device
 
@@ -169,6 +178,25 @@ class MegakernelDecoder:
             self._h, self._tok.data_ptr(), self._tok.data_ptr() + 4, stamps.data_ptr(),
             _stream_ptr()))
         return int(self._tok[1].item()), stamps
+
+    # stage columns of the reference's debug_ldg_decode_cycles (fused_decode_ldg_common.inl:51-69)
+    # filled from this kernel's phases; the stages it fuses (the input RMSNorm into the q|k|v
+    # GEMV, the q/k norm + RoPE into attention, the post norm into gate|up) read 0
+    _CYCLE_COLUMNS = (2, 3, 6, 7, 8, 9, 12, 13, 14, 15)
+
+    def debug_ldg_decode_cycles(self, input_token_id: int) -> torch.Tensor:
+        """One persistent decode step with stage timing, as the reference's
+        debug_ldg_decode_cycles (bindings_prefill.cpp:980-1043): an int64 CUDA tensor
+        [grid, num_layers, 16] of per-workgroup stage durations in the reference's stage columns
+        (MATVEC_QKV, MATVEC_SYNC2, ATTN, ATTN_SYNC, OPROJ_RESID, OPROJ_SYNC, GATE_UP,
+        GATE_UP_SYNC, DOWNPROJ, DOWNPROJ_SYNC).  Durations are in ticks of the 100 MHz
+        constant-rate clock (10 ns), not shader cycles."""
+        _, stamps = self.debug_decode_step_timing(input_token_id)
+        d = stamps[..., 1:] - stamps[..., :-1]
+        out = torch.zeros(stamps.shape[0], stamps.shape[1], 16, dtype=torch.int64,
+                          device=stamps.device)
+        out[..., list(self._CYCLE_COLUMNS)] = d
+        return out
 
     def set_position(self, position: int) -> None:
         """Moves the decode position (host and device) without touching the KV cache; the
@@ -279,6 +307,7 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
         self._graph = None
         self._graph_steps = 0
         self._graph_tokens = None
+        self._graph_failed = set()     # step counts whose capture failed (not retried)
 
     def prefill_step(self, input_token_ids) -> int:
         """Prefill positions 0..n-1, return the greedy next token, set position = n
@@ -345,6 +374,26 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
                                         self._logits.data_ptr(), _stream_ptr()))
         return int(self._tok[1].item()), self._logits.clone()
 
+    def debug_prefill_layers(self, input_token_ids):
+        """prefill_step that also returns the residual stream after every layer:
+        (next token, fp32 logits [vocab], bf16 [num_layers, n, hidden])."""
+        toks = torch.as_tensor(input_token_ids).reshape(-1)
+        n = int(toks.numel())
+        if n == 0:
+            raise RuntimeError("Empty input sequence")
+        if n > self.max_prefill_len:
+            raise RuntimeError(f"Prefill sequence length {n} exceeds maximum {self.max_prefill_len}")
+        if self._logits is None:
+            self._logits = torch.empty(self.vocab_size, dtype=torch.float32, device=self._tok.device)
+        d = toks.to(device=self._tok.device, dtype=torch.int32).contiguous()
+        trace = torch.empty(max(self.num_layers, 1), n, self.embed_weight.shape[1],
+                            dtype=torch.bfloat16, device=self._tok.device)
+        _lib.check(self._lib.mq_debug_prefill_layers(self._h, d.data_ptr(), n,
+                                                     self._tok.data_ptr() + 4,
+                                                     self._logits.data_ptr(), trace.data_ptr(),
+                                                     _stream_ptr()))
+        return int(self._tok[1].item()), self._logits.clone(), trace[:self.num_layers]
+
     def debug_prefill_buffers(self, n: int) -> dict:
         """Views (bf16) of the prefill buffers after a prefill of n tokens: h, xn, qkv, att, mlp
         (the last layer's values)."""
@@ -377,16 +426,24 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
     def decode_steps(self, first_token_id: int, num_steps: int) -> torch.Tensor:
         return self.decode_steps_cuda(first_token_id, num_steps).cpu()
 
+    @property
+    def graph_captured(self) -> bool:
+        """Whether the last decode_steps_cuda_graph call replayed a captured graph."""
+        return self._graph is not None
+
     def decode_steps_cuda_graph(self, first_token_id: int, num_steps: int) -> torch.Tensor:
         """decode_steps_cuda replayed from a captured HIP graph (rebuilt when num_steps changes;
-        bindings_prefill.cpp:1082-1150).  Falls back to the eager chain if capture fails."""
+        bindings_prefill.cpp:1082-1150).  Falls back to the eager chain if capture fails; a step
+        count whose capture failed is not captured again (graph_captured tells which ran)."""
         num_steps = int(num_steps)
         if num_steps <= 0:
             return torch.empty(0, dtype=torch.int32, device=self._tok.device)
         if self.position() + num_steps >= self.max_seq_len:
             raise RuntimeError("decode_steps_cuda_graph would exceed max_seq_len")
         if self._graph is None or self._graph_steps != num_steps:
-            if not self._capture(num_steps):
+            if num_steps in self._graph_failed or not self._capture(num_steps):
+                self._graph_failed.add(num_steps)
+                self._graph = None
                 return self.decode_steps_cuda(first_token_id, num_steps)
         self._graph_tokens[0] = self._check_token(first_token_id)
         self._graph.replay()
@@ -447,3 +504,14 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
                 return out[:kept], kept, 1
             nxt = int(toks[steps].item())
         return out[:gen], gen, 0
+
+
+class MegakernelFusedPrefillDecoder(MegakernelPrefillDecoder):
+    """The reference's short-prompt decoder class (bindings_fused_prefill.cpp:286-545; default
+    max_prefill_len 64, `max_prefill_len()` a method) on the same HIP prefill and decode."""
+
+    def __init__(self, embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight,
+                 cos_table, sin_table, num_layers, max_seq_len, max_prefill_len=64, **kwargs):
+        super().__init__(embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight,
+                         cos_table, sin_table, num_layers, max_seq_len,
+                         max_prefill_len=max_prefill_len, **kwargs)

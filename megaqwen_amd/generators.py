@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import torch
 
-from .decoder import MegakernelDecoder, MegakernelPrefillDecoder
+from .decoder import MegakernelDecoder, MegakernelFusedPrefillDecoder, MegakernelPrefillDecoder
 from .spec import get_active_model_spec
 from .weights import load_qwen3_weights
 
@@ -71,10 +71,11 @@ class MegakernelGenerator:
 class MegakernelPrefillGenerator:
     """Prefill the prompt, then greedy decode (megakernel_generators.py:67-128)."""
 
+    _decoder_cls = MegakernelPrefillDecoder
+
     def __init__(self, model_name="Qwen/Qwen3-0.6B", max_seq_len=2048, max_prefill_len=512):
         weights = load_qwen3_weights(model_name, max_seq_len=max_seq_len)
-        self.decoder = MegakernelPrefillDecoder(*_decoder_args(weights, max_seq_len),
-                                                max_prefill_len)
+        self.decoder = self._decoder_cls(*_decoder_args(weights, max_seq_len), max_prefill_len)
         self.tokenizer = weights["tokenizer"]
         self.max_seq_len = int(max_seq_len)
         self.max_prefill_len = int(max_prefill_len)
@@ -115,6 +116,8 @@ class MegakernelPrefillGenerator:
 class MegakernelFusedPrefillGenerator(MegakernelPrefillGenerator):
     """Name and defaults of the reference's small-prompt generator
     (megakernel_generators.py:131-190); runs the MFMA prefill."""
+
+    _decoder_cls = MegakernelFusedPrefillDecoder
 
     def __init__(self, model_name="Qwen/Qwen3-0.6B", max_seq_len=2048, max_prefill_len=64):
         super().__init__(model_name, max_seq_len=max_seq_len, max_prefill_len=max_prefill_len)

@@ -4,7 +4,8 @@ Only `tests/`, `__graft_entry__.smoke()` and `bench.py`'s `cpu_baseline` leg may
 module, and only as the checker / the timed CPU baseline.  The product path (`megaqwen_amd`)
 never imports it.
 
-It restates, in PyTorch-CPU fp32, what the reference computes:
+It restates, in PyTorch-CPU fp32 (or fp64 with the same rounding points, to measure the fp32
+evaluation's own spread), what the reference computes:
 
 * decode step (`mode="decode"`): the persistent decode kernel of the reference,
   csrc/megakernel/fused_decode_ldg_kernel.inl:43-137 driving the phases in
@@ -40,8 +41,8 @@ EPS = 1e-6
 
 
 def bf16(x: torch.Tensor) -> torch.Tensor:
-    """Round-to-nearest-even to bf16, returned as fp32 (as __float2bfloat16 then widening)."""
-    return x.to(torch.bfloat16).to(torch.float32)
+    """Round-to-nearest-even to bf16, returned in x's dtype (as __float2bfloat16 then widening)."""
+    return x.to(torch.bfloat16).to(x.dtype)
 
 
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float = EPS) -> torch.Tensor:
@@ -75,17 +76,24 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -> t
 
 
 class OracleModel:
-    """fp32 CPU model over bf16-representable weights.
+    """CPU model over bf16-representable weights, in fp32 (the reference's arithmetic) or, with
+    `dtype=torch.float64`, in fp64 with the same bf16 rounding points.  The fp64 evaluation
+    measures how far the fp32 oracle's own rounding of sums moves its results (the spread the
+    GPU tests' tolerances are set against); it is not a different model.
 
-    weights: dict from megaqwen_amd.synthetic.make_weights (any float dtype; converted to fp32).
+    weights: dict from megaqwen_amd.synthetic.make_weights (any float dtype; converted to `dtype`).
     cos/sin: [max_seq, D] tables (bf16 values as in the reference, or fp32 for the HF pin).
     """
 
     def __init__(self, weights: dict, spec: dict, cos: torch.Tensor, sin: torch.Tensor,
-                 max_seq_len: int, round_bf16: bool = True, threads: int | None = None):
+                 max_seq_len: int, round_bf16: bool = True, threads: int | None = None,
+                 dtype: torch.dtype = torch.float32):
         if threads is not None:
             torch.set_num_threads(int(threads))
-        f = lambda t: t.to(torch.float32).contiguous()
+        if dtype not in (torch.float32, torch.float64):
+            raise ValueError("dtype must be torch.float32 or torch.float64")
+        self.dtype = dtype
+        f = lambda t: t.to(dtype).contiguous()
         self.spec = dict(spec)
         self.H = int(spec["hidden_size"])
         self.I = int(spec["intermediate_size"])
@@ -106,8 +114,8 @@ class OracleModel:
         self.sin = f(sin)
         self.max_seq_len = int(max_seq_len)
         self.round = bool(round_bf16)
-        self.k_cache = torch.zeros(self.L, self.nkv, self.max_seq_len, self.D)
-        self.v_cache = torch.zeros(self.L, self.nkv, self.max_seq_len, self.D)
+        self.k_cache = torch.zeros(self.L, self.nkv, self.max_seq_len, self.D, dtype=dtype)
+        self.v_cache = torch.zeros(self.L, self.nkv, self.max_seq_len, self.D, dtype=dtype)
         self.position = 0
 
     def _r(self, x: torch.Tensor) -> torch.Tensor:
@@ -179,43 +187,52 @@ class OracleModel:
         R = self._r
         h = self.embed[toks].clone()                          # [n, H]
         if embeds is not None:
-            e = torch.as_tensor(embeds).float().reshape(-1, h.shape[1])
+            e = torch.as_tensor(embeds).to(self.dtype).reshape(-1, h.shape[1])
             if e.shape[0] <= 0 or embeds_start < 0 or embeds_start + e.shape[0] > n:
                 raise RuntimeError("Invalid audio_start_idx/audio_len for the given seq_len")
             h[embeds_start:embeds_start + e.shape[0]] = e
-        c, s = self.cos[:n].unsqueeze(1), self.sin[:n].unsqueeze(1)
-        causal = torch.ones(n, n, dtype=torch.bool).tril()
-        for li, w in enumerate(self.layers):
-            resid = h
-            nrm = R(rms_norm(h, w["input_ln"]))
-            q = R(nrm @ w["q"].T).view(n, self.nq, self.D)
-            k = R(nrm @ w["k"].T).view(n, self.nkv, self.D)
-            v = R(nrm @ w["v"].T).view(n, self.nkv, self.D)
-            q = R(rope(rms_norm(q, w["q_norm"]), c, s))
-            k = R(rope(rms_norm(k, w["k_norm"]), c, s))
-            self.k_cache[li, :, :n] = k.transpose(0, 1)
-            self.v_cache[li, :, :n] = v.transpose(0, 1)
-            qh = q.transpose(0, 1)                                          # [nq, n, D]
-            kh = k.transpose(0, 1).repeat_interleave(self.group, dim=0)     # [nq, n, D]
-            vh = v.transpose(0, 1).repeat_interleave(self.group, dim=0)
-            sc = torch.matmul(qh, kh.transpose(-1, -2)) * self.scale
-            sc = sc.masked_fill(~causal, float("-inf"))
-            att = torch.matmul(torch.softmax(sc, dim=-1), vh)               # [nq, n, D]
-            att = R(att.transpose(0, 1).reshape(n, self.nq * self.D))
-            o = R(att @ w["o"].T)
-            h = R(o + resid)
-            resid = h
-            n2 = R(rms_norm(h, w["post_ln"]))
-            g = R(n2 @ w["gate"].T)
-            u = R(n2 @ w["up"].T)
-            m = R(silu(g) * u)
-            d = R(m @ w["down"].T)
-            h = R(d + resid)
+        for li in range(self.L):
+            h = self.prefill_layer(li, h)
         hf = R(rms_norm(h[-1], self.final_norm))
         logits = self.lm_head @ hf
         self.position = n
         tok = int(torch.argmax(logits).item())
         return (tok, logits) if return_logits else tok
+
+    def prefill_layer(self, li: int, h: torch.Tensor) -> torch.Tensor:
+        """Prefill layer li on the residual stream h [n, H] (bf16 values) at positions 0..n-1
+        (fused_prefill_launch.inl:245-657): writes K/V rows 0..n-1 of layer li and returns the
+        layer output [n, H].  Every GEMM output and elementwise result is rounded to bf16."""
+        R = self._r
+        w = self.layers[li]
+        n = int(h.shape[0])
+        c, s = self.cos[:n].unsqueeze(1), self.sin[:n].unsqueeze(1)
+        causal = torch.ones(n, n, dtype=torch.bool).tril()
+        resid = h
+        nrm = R(rms_norm(h, w["input_ln"]))
+        q = R(nrm @ w["q"].T).view(n, self.nq, self.D)
+        k = R(nrm @ w["k"].T).view(n, self.nkv, self.D)
+        v = R(nrm @ w["v"].T).view(n, self.nkv, self.D)
+        q = R(rope(rms_norm(q, w["q_norm"]), c, s))
+        k = R(rope(rms_norm(k, w["k_norm"]), c, s))
+        self.k_cache[li, :, :n] = k.transpose(0, 1)
+        self.v_cache[li, :, :n] = v.transpose(0, 1)
+        qh = q.transpose(0, 1)                                          # [nq, n, D]
+        kh = k.transpose(0, 1).repeat_interleave(self.group, dim=0)     # [nq, n, D]
+        vh = v.transpose(0, 1).repeat_interleave(self.group, dim=0)
+        sc = torch.matmul(qh, kh.transpose(-1, -2)) * self.scale
+        sc = sc.masked_fill(~causal, float("-inf"))
+        att = torch.matmul(torch.softmax(sc, dim=-1), vh)               # [nq, n, D]
+        att = R(att.transpose(0, 1).reshape(n, self.nq * self.D))
+        o = R(att @ w["o"].T)
+        h = R(o + resid)
+        resid = h
+        n2 = R(rms_norm(h, w["post_ln"]))
+        g = R(n2 @ w["gate"].T)
+        u = R(n2 @ w["up"].T)
+        m = R(silu(g) * u)
+        d = R(m @ w["down"].T)
+        return R(d + resid)
 
     def prefill_hidden_all(self, tokens):
         """fp32 logits for EVERY prompt position (no mutation of position semantics beyond

@@ -46,3 +46,57 @@ def build_pair(num_layers: int, vocab: int, max_seq: int, seed: int = 0, norm_ji
 def top2_margin(logits: torch.Tensor) -> float:
     v = torch.topk(logits.float(), 2).values
     return float(v[0] - v[1])
+
+
+def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 values at |x| (8 significant bits)."""
+    e = torch.floor(torch.log2(x.abs().clamp_min(1e-30)))
+    return torch.pow(2.0, e - 7)
+
+
+def oracle_kv_row(orc, li: int, x: torch.Tensor, pos: int):
+    """The bf16 K and V rows the oracle's decode layer li writes at `pos` for input x."""
+    from oracle.ref_cpu import bf16, rms_norm, rope
+    w = orc.layers[li]
+    n = rms_norm(x, w["input_ln"])
+    k = rope(rms_norm((w["k"] @ n).view(orc.nkv, orc.D), w["k_norm"]), orc.cos[pos], orc.sin[pos])
+    v = (w["v"] @ n).view(orc.nkv, orc.D)
+    return bf16(k), bf16(v)
+
+
+def check_decode_step_layerwise(dec, orc, token: int, pos: int, exact_frac: float = 0.99):
+    """One GPU decode step at `pos` checked layer by layer against the oracle.
+
+    The oracle takes over the GPU's KV cache (including the row the GPU wrote for `pos`) and, at
+    every layer, the GPU's input hidden state, so rounding-order differences cannot compound.
+    Bounds: new K/V rows within one bf16 ulp + 2e-5 x max|row| of the oracle's own rows from the
+    same input; layer outputs within one bf16 ulp + 2e-5 x max|output|, and at least `exact_frac`
+    of all layer-output elements bit-equal; logits of the GPU's final hidden state within 1e-4 of
+    the GPU's own logits.  Returns (gpu token, gpu logits)."""
+    assert dec.position() == pos
+    tok, lg, trace = dec.debug_decode_step_layers(token)
+    trace = trace.cpu()
+    kc = dec.k_cache.float().cpu()
+    vc = dec.v_cache.float().cpu()
+    orc.k_cache = kc
+    orc.v_cache = vc
+    x = orc.embed[token].clone()
+    exact = 0
+    L = orc.L
+    for li in range(L):
+        own = oracle_kv_row(orc, li, x, pos)
+        for got, ref in ((kc[li, :, pos], own[0]), (vc[li, :, pos], own[1])):
+            kb = bf16_ulp(ref) + 2e-5 * ref.abs().amax(dim=-1, keepdim=True)
+            assert ((got - ref).abs() <= kb).all(), ("kv row", pos, li)
+        y = orc.decode_layer(li, x, pos, write_kv=False)
+        g = trace[li]
+        bound = bf16_ulp(y) + 2e-5 * float(y.abs().max())
+        bad = (g - y).abs() > bound
+        assert not bad.any(), ("layer", pos, li, g[bad][:4].tolist(), y[bad][:4].tolist())
+        exact += int((g == y).sum())
+        x = g
+    assert exact >= exact_frac * L * trace.shape[1], (pos, exact)
+    ref = orc.lm_head_logits(trace[-1])
+    assert float((lg.cpu() - ref).abs().max()) < 1e-4, pos
+    assert tok == int(torch.argmax(lg))
+    return tok, lg

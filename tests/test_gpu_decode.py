@@ -10,11 +10,12 @@ import pytest
 import torch
 
 from megaqwen_amd.synthetic import make_tokens
+from tests import tolerances as T
 from tests.helpers import build_pair, top2_margin
 
 pytestmark = pytest.mark.gpu
 
-TOL = 2e-2
+TOL = T.DECODE_LOGITS
 
 
 def _run_teacher_forced(dec, orc, tokens, mode):
@@ -110,6 +111,16 @@ def test_decode_early_kv_variant(monkeypatch):
                                   for u in [t] + toks[:4].tolist()]))
         dec.check()
     assert torch.equal(longs[0], longs[1])
+    # cache lengths 897-899 split into 31 chunks of 29, which leaves the last workgroup of every
+    # group without a chunk: its gate|up weights must still be fetched (regression test)
+    idle = []
+    for dec in (dec1, dec0):
+        dec.reset()
+        t = dec.prefill_step(make_tokens(895, sp["vocab_size"], seed=13))
+        idle.append(torch.stack([dec.decode_step_with_logits(int(u))[1]
+                                 for u in [t] + toks[:6].tolist()]))
+        dec.check()
+    assert torch.equal(idle[0], idle[1])
 
 
 def test_decode_long_context_chunks(small):
@@ -233,9 +244,9 @@ def OracleModelRow(orc, li, x, pos):
 def test_decode_28_layers_free_running(full):
     """Free-running teacher-forced comparison of the full 28-layer model.  At this depth the
     random-init model amplifies a single bf16-ulp flip of one hidden element to ~3e-2 on the
-    logits, and the oracle's own fp32 and fp64 evaluations differ by ~2.7e-2, so the bound here
-    is 6e-2 (about twice that intrinsic spread); the 2e-2 bar is enforced by the 2-layer tests
-    above and the layer-by-layer test."""
+    logits: the oracle's own fp32 and fp64 evaluations of this case differ by 2.76e-2
+    (tests/test_oracle_spread.py), so the bound is T.DECODE_28L = 5.5e-2, twice that spread; the
+    2e-2 bar is enforced by the 2-layer tests above and the layer-by-layer tests."""
     dec, orc, sp, _ = full
     toks = make_tokens(8, sp["vocab_size"], seed=0)
     dec.set_mode("persistent")
@@ -247,7 +258,7 @@ def test_decode_28_layers_free_running(full):
         otok, olg = orc.decode_step(int(t))
         err = float((lg.cpu() - olg).abs().max())
         worst = max(worst, err)
-        assert err <= 6e-2, (i, err)
+        assert err <= T.DECODE_28L, (i, err)
         if top2_margin(olg) > 2 * err + 1e-6:
             assert tok == otok, (i, tok, otok)
     print(f"28-layer free-running worst logit error {worst:.3e}")
@@ -272,6 +283,7 @@ def test_decode_steps_chain_and_graph(small):
     assert host == ref
     dec.reset()
     g1 = dec.decode_steps_cuda_graph(first, 12).cpu().tolist()
+    assert dec.graph_captured, "the HIP graph capture failed; the eager chain ran instead"
     torch.cuda.synchronize()
     g2 = dec.decode_steps_cuda_graph(g1[-1], 12).cpu().tolist()
     assert g1 + g2 == ref and dec.position() == 24

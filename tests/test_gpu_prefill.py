@@ -7,11 +7,13 @@ q/k norm and RoPE) within one bf16 ulp plus 5e-4 absolute and >= 98% bit-equal. 
 term covers one legitimate rounding flip of the bf16 RMSNorm output: fp32 summation order moves
 rstd by ~1e-7, which can flip an element of xn by one bf16 ulp (~8e-3 at |xn| ~ 1-2), moving a
 dot product by |w| * ulp ~ 2e-4.  Deeper layers compound such flips through bf16 rounding after
-every op, so they are checked through the last-position logits.  Prefill rounds to bf16 after
-every op, so its logits carry more rounding noise than decode's: the oracle's own prefill run in
-fp32 and in fp64 arithmetic (same bf16 rounding points) differs by 1.7e-2 - 2.0e-2 already at 2
-layers (n = 7..512), so the prefill logits bound is 4e-2 (twice that spread); decode continuing
-after prefill is held to the north-star 2e-2 (teacher-forced).  K rows pass through RoPE, whose
+every op, so here they are checked through the last-position logits.  Prefill rounds to bf16
+after every op, so its logits carry more rounding noise than decode's: the oracle's own prefill run in
+fp32 and in fp64 arithmetic (same bf16 rounding points) differs by 1.69e-2 - 2.03e-2 already at
+2 layers (n = 7..512; tests/test_oracle_spread.py), so the prefill logits bound is
+T.PREFILL_2L = 4e-2 (twice that spread); decode continuing after prefill is held to the
+north-star 2e-2 (teacher-forced).  Deeper prefill layers are checked one by one in
+tests/test_gpu_configs.py (config 4).  K rows pass through RoPE, whose
 a*c - b*s can cancel: a one-ulp input flip of a large element becomes several ulps of a small
 output, so K is bounded by ulp(ref) + ulp(max |k| of the head).
 """
@@ -19,6 +21,7 @@ import pytest
 import torch
 
 from megaqwen_amd.synthetic import make_tokens
+from tests import tolerances as T
 from tests.helpers import build_pair, top2_margin
 
 pytestmark = pytest.mark.gpu
@@ -63,7 +66,7 @@ def test_prefill_matches_oracle(small, n):
     assert _close_bf16(kc[0, :, :n], orc.k_cache[0, :, :n], head_ulp=True), "k"
     err = float((lg.cpu() - olg).abs().max())
     print(f"prefill n={n}: logit error {err:.3e}")
-    assert err <= 4e-2, err
+    assert err <= T.PREFILL_2L, err
     if top2_margin(olg) > 2 * err + 1e-6:
         assert tok == otok
     dec.check()
@@ -81,7 +84,7 @@ def test_decode_after_prefill(small):
         tok, lg = dec.decode_step_with_logits(t)
         otok, olg = orc.decode_step(t)
         err = float((lg.cpu() - olg).abs().max())
-        assert err <= 2e-2, (i, err)
+        assert err <= T.DECODE_LOGITS, (i, err)
         if top2_margin(olg) > 2 * err + 1e-6:
             assert tok == otok
     assert dec.position() == 57
@@ -177,7 +180,7 @@ def test_prefill_asr_embedding_patch(small):
     tok2, lg = dec.prefill_asr(toks, audio.cuda(), a, return_logits=True)
     err = float((lg.cpu() - olg).abs().max())
     print(f"prefill_asr: logit error {err:.3e}")
-    assert tok2 == tok and err <= 4e-2
+    assert tok2 == tok and err <= T.PREFILL_2L
     if top2_margin(olg) > 2 * err + 1e-6:
         assert tok == otok
     dec.reset()
@@ -202,8 +205,9 @@ def test_prefill_errors(small):
 
 def test_prefill_28_layers_real_shape():
     """28 layers, 512-token prompt (BASELINE config 4 shape): layer-0 KV rows tightly, the final
-    logits loosely (at this depth a single bf16 flip moves the logits by ~3e-2, see
-    test_gpu_decode.py)."""
+    logits within T.PREFILL_28L = 7e-2, twice the oracle's own fp32-vs-fp64 spread of 3.66e-2 on
+    this case (tests/test_oracle_spread.py).  Every layer is checked on its own in
+    tests/test_gpu_configs.py."""
     dec, orc, sp, _ = build_pair(28, 151936, 520, seed=0, max_prefill=512)
     toks = make_tokens(512, sp["vocab_size"], seed=1)
     tok, lg = dec.prefill_step_with_logits(toks)
@@ -213,5 +217,21 @@ def test_prefill_28_layers_real_shape():
                        head_ulp=True)
     err = float((lg.cpu() - olg).abs().max())
     print(f"28-layer prefill logit error {err:.3e}")
-    assert err <= 1e-1
+    assert err <= T.PREFILL_28L
+    dec.check()
+
+
+def test_prefill_out_of_vocab_id_sets_device_error(small):
+    """Token ids stay on the device through the C ABI (mq_prefill), so the embedding gather checks
+    them there: an id outside the vocabulary reads row 0 instead of memory past the table and
+    sets the error flag that mq_decoder_check reports; reset() clears it."""
+    dec = small[0]
+    dec.reset()
+    d = torch.tensor([5, dec.vocab_size, 7], dtype=torch.int32, device="cuda")
+    rc = dec._lib.mq_prefill(dec._h, d.data_ptr(), 3, dec._tok.data_ptr() + 4, None,
+                             torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    with pytest.raises(RuntimeError):
+        dec.check()
+    dec.reset()
     dec.check()
