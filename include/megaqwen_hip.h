@@ -192,6 +192,16 @@ int mq_op_qkv_rope(mq_decoder* dec, int layer, const void* d_x_bf16, int pos, fl
  *     -> fp32 [Hq*D] (fused_decode_ldg_common.inl:417-794). */
 int mq_op_attention(mq_decoder* dec, int layer, const float* d_q, int cache_len, float* d_out,
                     void* stream);
+/* (b') Allocation-free variant of mq_op_attention.  No counterpart in the reference: it is for
+ *     callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ *     loops, harnesses that forbid hipMalloc).  Same inputs, outputs and kernels as
+ *     mq_op_attention, but the split-K partials live in a static device array of the library
+ *     (640 KiB on each GPU it runs on, held until the process ends) instead of the decoder's
+ *     workspace, and the call allocates nothing.  Calls that overlap on one GPU share that array
+ *     and race.  Rejects cache lengths whose partials would exceed it (more than 64 position
+ *     chunks per kv head) with MQ_ERR_INVALID_ARG. */
+int mq_op_attention_noalloc(mq_decoder* dec, int layer, const float* d_q, int cache_len,
+                            float* d_out, void* stream);
 /* (c) x_out = bf16(W_down(silu(W_gate n) * W_up n) + a), n = RMSNorm(a) * post_ln
  *     (fused_decode_ldg_mlp.inl:70-217).  a: fp32 [H]. */
 int mq_op_mlp(mq_decoder* dec, int layer, const float* d_a, void* d_x_out_bf16, void* stream);

@@ -453,6 +453,23 @@ int mq_op_attention(mq_decoder* dec, int layer, const float* d_q, int cache_len,
   return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%d)", rc);
 }
 
+int mq_op_attention_noalloc(mq_decoder* dec, int layer, const float* d_q, int cache_len,
+                            float* d_out, void* stream) {
+  if (dec == nullptr || d_q == nullptr || d_out == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "NULL argument");
+  if (layer < 0 || layer >= dec->p.num_layers || cache_len < 1 || cache_len > dec->p.max_seq)
+    return fail(MQ_ERR_INVALID_ARG, "layer %d / cache_len %d out of range", layer, cache_len);
+  if (mq_attn_nchunks(cache_len, dec->grid) > MQ_MAX_CHUNKS)
+    return fail(MQ_ERR_INVALID_ARG,
+                "cache_len %d needs more split-K partials than the static scratch holds (%d "
+                "chunks per kv head)", cache_len, MQ_MAX_CHUNKS);
+  int rc = mq_launch_op_attention_noalloc(dec->p, layer, d_q, cache_len, d_out, dec->grid,
+                                          static_cast<hipStream_t>(stream));
+  if (rc == -1 || rc == -2)
+    return fail(MQ_ERR_HIP, "device address of the static scratch unavailable (%d)", rc);
+  return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%d)", rc);
+}
+
 int mq_op_mlp(mq_decoder* dec, int layer, const float* d_a, void* d_x_out_bf16, void* stream) {
   if (dec == nullptr || d_a == nullptr || d_x_out_bf16 == nullptr)
     return fail(MQ_ERR_INVALID_ARG, "NULL argument");

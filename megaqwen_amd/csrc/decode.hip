@@ -29,6 +29,7 @@
 
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 // Thread index hidden behind an empty asm so that per-lane address arithmetic is recomputed in
@@ -1636,6 +1637,47 @@ int mq_launch_op_attention(const MqDecodeParams& p, int layer, const float* q_ha
   mq_op_attn_kernel<<<grid, MQ_THREADS, 0, stream>>>(p, layer, q_hat, cache_len, nch);
   mq_op_merge_kernel<<<MQ_NKV, MQ_THREADS, 0, stream>>>(p, nch, att_out);
   return launch_status();
+}
+
+// ------------------------------------------------------ allocation-free attention op
+// Device memory of mq_launch_op_attention_noalloc: one MqScratch (its split-K partials are the
+// only part the attention op uses) in a file-scope device array, so callers that cannot allocate
+// (code under graph capture, serving loops) need no workspace.  Each GPU the library runs on
+// holds its own copy until the process ends.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is only a stand-in for the symbol): the device address of each
+// GPU's copy comes from hipGetSymbolAddress, resolved once per device with that device current.
+static __device__ __align__(256) unsigned char scratch[MQ_NOALLOC_SCRATCH_BYTES];
+static_assert(sizeof(MqScratch) <= MQ_NOALLOC_SCRATCH_BYTES, "scratch holds one MqScratch");
+
+#define MQ_NOALLOC_MAX_DEVICES 64
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MQ_NOALLOC_MAX_DEVICES] = {};
+
+// Device address of the current device's `scratch` (resolved on the first call per device).
+static int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MQ_NOALLOC_MAX_DEVICES) return -1;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr)
+      return -2;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+int mq_launch_op_attention_noalloc(const MqDecodeParams& p, int layer, const float* q_hat,
+                                   int cache_len, float* att_out, int grid, hipStream_t stream) {
+  if (mq_attn_nchunks(cache_len, grid) > MQ_MAX_CHUNKS) return -3;
+  void* s = nullptr;
+  const int rc = scratch_address(&s);
+  if (rc != 0) return rc;
+  MqDecodeParams pc = p;
+  pc.s = static_cast<MqScratch*>(s);
+  // every partial the merge reads is written by the attention kernel first: nothing to clear
+  return mq_launch_op_attention(pc, layer, q_hat, cache_len, att_out, grid, stream);
 }
 
 int mq_launch_op_mlp(const MqDecodeParams& p, int layer, const float* a_in, bf16_t* x_out,

@@ -125,6 +125,11 @@ int mq_launch_op_qkv_rope(const MqDecodeParams& p, int layer, const bf16_t* x, i
                           float* q_out, int grid, hipStream_t stream);
 int mq_launch_op_attention(const MqDecodeParams& p, int layer, const float* q_hat, int cache_len,
                            float* att_out, int grid, hipStream_t stream);
+// mq_launch_op_attention with p.s replaced by the library's static device scratch (no
+// allocation, no workspace).  Calls that overlap on one GPU share that scratch and race.
+#define MQ_NOALLOC_SCRATCH_BYTES (640u * 1024u)
+int mq_launch_op_attention_noalloc(const MqDecodeParams& p, int layer, const float* q_hat,
+                                   int cache_len, float* att_out, int grid, hipStream_t stream);
 int mq_launch_op_mlp(const MqDecodeParams& p, int layer, const float* a_in, bf16_t* x_out,
                      int grid, hipStream_t stream);
 int mq_launch_op_layer(const MqDecodeParams& p, int layer, const bf16_t* x, int pos,
