@@ -36,7 +36,7 @@ int fail(int code, const char* fmt, ...) {
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct Layout {
-  size_t state, layers, scratch, prefill, total;
+  size_t state, layers, scratch, xch, prefill, total;
 };
 
 Layout layout_of(const mq_model_desc* d) {
@@ -44,7 +44,8 @@ Layout layout_of(const mq_model_desc* d) {
   L.state = 0;
   L.layers = align_up(L.state + sizeof(MqState), 256);
   L.scratch = align_up(L.layers + sizeof(MqLayerW) * (size_t)d->num_layers, 256);
-  L.prefill = align_up(L.scratch + sizeof(MqScratch), 256);
+  L.xch = align_up(L.scratch + sizeof(MqScratch), 256);
+  L.prefill = align_up(L.xch + sizeof(MqExchange), 256);
   L.total = align_up(L.prefill + mq_prefill_workspace_bytes(d->max_prefill_len), 256);
   return L;
 }
@@ -202,6 +203,7 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   p.kc = static_cast<bf16_t*>(k_cache);
   p.vc = static_cast<bf16_t*>(v_cache);
   p.s = reinterpret_cast<MqScratch*>(ws + lay.scratch);
+  p.x = reinterpret_cast<MqExchange*>(ws + lay.xch);
   p.st = reinterpret_cast<MqState*>(ws + lay.state);
   p.scale_log2 = (float)(1.4426950408889634 / sqrt((double)MQ_D));
   p.attn_local_max = env_int("MEGAQWEN_ATTN_LOCAL_MAX", MQ_ATT_LOCAL_DEFAULT, 0, 1 << 20);
@@ -216,7 +218,7 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   dec->kv_bytes = (size_t)desc->num_layers * MQ_NKV * (size_t)desc->max_seq_len * MQ_D * 2;
   dec->ws = ws;
   mq_prefill_bind(&dec->pf, ws + lay.prefill, desc->max_prefill_len);
-  if (mq_launch_fill_state(p.st, 0, nullptr, true) != 0 ||
+  if (mq_launch_clear_state(p.st, p.x, nullptr) != 0 ||
       hipStreamSynchronize(nullptr) != hipSuccess) {
     delete dec;
     return fail(MQ_ERR_HIP, "state initialisation failed");
@@ -235,7 +237,7 @@ int mq_decoder_reset(mq_decoder* dec, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (mq_launch_zero(dec->p.kc, dec->kv_bytes, s) != 0 ||
       mq_launch_zero(dec->p.vc, dec->kv_bytes, s) != 0 ||
-      mq_launch_fill_state(dec->p.st, 0, s, true) != 0)
+      mq_launch_clear_state(dec->p.st, dec->p.x, s) != 0)
     return fail(MQ_ERR_HIP, "reset kernels failed to launch");
   dec->pos = 0;
   return MQ_OK;

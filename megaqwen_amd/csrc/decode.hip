@@ -57,8 +57,8 @@ static_assert(MQ_SYNC_WAVE == MQ_CWAVES && MQ_CWAVES + 1 == MQ_WAVES, "one sync 
 #define LDS_A 5632        // [1024] a = layer input + attention block output (MLP residual)
 #define LDS_ATTH 0        // [256]  merged attention output of the group's two query heads
 #define LDS_AROW 6656     // [MQ_CWAVES][256] attention: unnormalised p.V of each compute wave
-#define LDS_AL (LDS_AROW + MQ_CWAVES * 256)   // [MQ_CWAVES][2] sums of p of each compute wave
-#define MQ_LDS_FLOATS (LDS_AL + MQ_CWAVES * 2)
+#define LDS_QA (LDS_AROW + MQ_CWAVES * 256)   // [4][64][8] bf16: q-hat as the MFMA A operand
+#define MQ_LDS_FLOATS (LDS_QA + 4 * 64 * 4)
 
 // Balanced contiguous row range of workgroup `wg` out of `G` for an `n`-row matrix.
 MQ_DEV void row_range(int n, int wg, int G, int& r0, int& nr) {
@@ -169,6 +169,53 @@ MQ_DEV void wave_copy_bf16_1024(float* dst, const bf16_t* src) {
   for (int i = 0; i < 2; ++i) unpack8(v[i], dst + 8 * (lane + 64 * i));
 }
 
+// Sync wave: polls P (value, epoch) words per lane (word idx(i) of `src` for lane's i < P) until
+// every one carries epoch e, then hands out(i, value).  Only words still carrying an old epoch are
+// loaded again.  e == 0 takes the words as they are (written by an earlier kernel of the
+// one-kernel-per-phase mode).  A set error flag (read on every 16th round) or the spin bound ends
+// the wait early; the step's results are then invalid and mq_decoder_check reports it.
+template <int P, class Idx, class Out>
+MQ_DEV void x_poll(const uint64_t* src, Idx idx, uint32_t e, MqSync* sy, Out out) {
+  const int lane = lane_id();
+  uint64_t v[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) v[i] = ld_coh64(src + idx(i));
+  if (e != 0) {
+    uint32_t spins = 0;
+    while (true) {
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < P; ++i) ok = ok && xepoch(v[i]) == e;
+      if (__all(ok)) break;
+      uint32_t ev = 0;
+      if (lane == 0 && (spins & 15) == 15)
+        ev = __hip_atomic_load(&sy->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_amdgcn_readlane(ev, 0) != 0) break;
+      if (++spins > MQ_SPIN_LIMIT) {
+        if (lane == 0)
+          __hip_atomic_store(&sy->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int i = 0; i < P; ++i)
+        if (xepoch(v[i]) != e) v[i] = ld_coh64(src + idx(i));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < P; ++i) out(i, xvalue(v[i]));
+}
+// The N contiguous words of src into LDS dst (and dst2 if given) as fp32.
+template <int N>
+MQ_DEV void x_gather(float* dst, float* dst2, const uint64_t* src, uint32_t e, MqSync* sy) {
+  static_assert(N % 64 == 0, "whole words per lane");
+  const int lane = lane_id();
+  x_poll<N / 64>(src, [&](int i) { return lane + 64 * i; }, e, sy, [&](int i, float v) {
+    dst[lane + 64 * i] = v;
+    if (dst2 != nullptr) dst2[lane + 64 * i] = v;
+  });
+}
+
 // Phase boundary.  Compute waves arrive with this phase's dot products in LDS and the next
 // phase's weight prefetch in flight.  The sync wave then runs `epilogue()` (finishes this
 // phase's outputs and publishes them with coherent stores), waits for those stores, runs the
@@ -244,88 +291,132 @@ MQ_DEV void qkv_publish(float* qkv, int wg, int G, const float* lds) {
 
 // ------------------------------------------------------------------------- P2: attention
 // LDS carve of the attention phase (floats).
-#define ALDS_RAW 0        // [512] raw q(2 heads) | k | v of this kv head (sync wave input)
-#define ALDS_QS 512       // [256] rotated q of the two query heads
+// [0, 256): LDS_ATTH, the attention output of a single-chunk (local) item
+#define ALDS_QS 512       // [256] rotated q of the two query heads (sync wave input)
 #define ALDS_KN 768       // [128] new-position k-hat (bf16 values)
 #define ALDS_VN 896       // [128] new-position v (bf16 values)
-#define ALDS_PRM 1024     // [512] q_norm | k_norm | cos row | sin row of this step, as fp32
 #define ALDS_WML 1536     // [MQ_CWAVES][4] per-wave m0, m1, l0, l1
 #define ALDS_STAT 1568    // m[2], l[2] of the item
+#define ALDS_SNEW 1576    // [2] scores (log2 domain) of the new position for both query heads
 #define ALDS_ORED 1584    // [MQ_CWAVES][256] per-wave unnormalised outputs; the item's in [0, 256)
-#define ALDS_WSC (ALDS_ORED + MQ_CWAVES * 256)   // [MQ_CWAVES][2][32] each wave's scores
-// The merge of several chunks runs after this item's partial has been published and after the
-// prologue's parameters have been used, so it reuses the parameter area.
-#define ALDS_MW ALDS_PRM                         // merge: (m, l)[2][64] then weights [2][64]
+#define ALDS_WSC (ALDS_ORED + MQ_CWAVES * 256)   // [MQ_CWAVES][32][2] each wave's weights
+// The merge of several chunks runs after this item's partial has been published, so it reuses
+// the per-wave areas.
+#define ALDS_MW 1024                             // merge: (m, l)[2][64] then weights [2][64]
 #define ALDS_MSUM (ALDS_MW + 512)                // merge: [4][2][128] partial sums
 static_assert(ALDS_WSC + MQ_CWAVES * 64 <= MQ_LDS_FLOATS, "attention LDS carve");
 static_assert(ALDS_MSUM + 1024 <= MQ_LDS_FLOATS, "attention merge LDS carve");
 static_assert(ALDS_MSUM + 1024 <= ALDS_ORED + MQ_CWAVES * 256, "merge stays in the phase carve");
 
-// q/k RMSNorm over one head held as (lane, lane + 64) of one wave, then rotate-half RoPE with
-// the bf16 table row (fused_decode_ldg_common.inl:268-394):
+// q/k RMSNorm of one head held by one wave as two consecutive dims per lane (lane l: dims 2l,
+// 2l + 1), then rotate-half RoPE with the bf16 table row (fused_decode_ldg_common.inl:268-394):
 //   o_i = x_i c_i - x_{i+64} s_i,  o_{i+64} = x_i s_{i+64} + x_{i+64} c_{i+64}.
-// nw, cs, sn: norm weight, cos row and sin row as fp32 in LDS.
-MQ_DEV void head_norm_rope(float& lo, float& hi, const float* nw, const float* cs,
-                           const float* sn) {
-  const int lane = lane_id();
-  const float ss = wave_sum(lo * lo + hi * hi);
+// The RoPE partner of lane l's dims is lane l ^ 32 (dims +- 64), one v_permlane32_swap away.
+// w, c, s: this lane's two norm weights, cos and sin values.
+MQ_DEV float2 head_norm_rope2(float2 x, float2 w, float2 c, float2 s) {
+  const float ss = wave_sum(x.x * x.x + x.y * x.y);
   const float r = rsqrtf(ss * (1.0f / MQ_D) + MQ_EPS);
-  const float a = lo * r * nw[lane];
-  const float b = hi * r * nw[lane + 64];
-  lo = a * cs[lane] - b * sn[lane];
-  hi = a * sn[lane + 64] + b * cs[lane + 64];
+  const float a0 = x.x * r * w.x, a1 = x.y * r * w.y;
+  const float2 p0 = swap32(a0), p1 = swap32(a1);     // (lanes 0-31 | 32-63), both orders
+  const bool low = lane_id() < 32;                    // dims < 64
+  const float b0 = low ? p0.y : p0.x, b1 = low ? p1.y : p1.x;   // partner lane's values
+  return low ? make_float2(a0 * c.x - b0 * s.x, a1 * c.y - b1 * s.y)
+             : make_float2(b0 * s.x + a0 * c.x, b1 * s.y + a1 * c.y);
 }
 
 MQ_DEV float* part_ptr(float* part, int h, int c, int j) {
   return part + ((size_t)(h * MQ_MAX_CHUNKS + c) * MQ_GQA + j) * MQ_PART_STRIDE;
 }
 
-// Sync-wave input of an attention item, one memory round trip: raw q of query heads 2h, 2h+1,
-// k and v of kv head h (coherent loads of the q|k|v vector), plus the read-only parameters of the
-// prologue (q_norm and k_norm weights of the layer, RoPE table rows of the position).
-MQ_DEV void attn_input(const float* qkv, const bf16_t* qn, const bf16_t* kn, const bf16_t* cs,
-                       const bf16_t* sn, int h, float* lds) {
+// q-hat of both query heads as the A operand of v_mfma_f32_16x16x32_bf16 in LDS_QA: A rows
+// 4 hh + t (hh = query head, t = 0, 1, 2) hold the bf16 parts q = hi + mid + lo (residuals exact
+// in fp32, so the three products with a bf16 key sum to the fp32 q . k up to ~2^-26 relative);
+// rows 3 and 7..15 stay zero.  Lane l of the calling wave holds dims 2l, 2l + 1 of each head.
+// Element (row r, dim d) of k-step s = d / 32 sits at lane r + 16 ((d % 32) / 8), entry d % 8.
+MQ_DEV void q_operand_store(float2 q0, float2 q1, float* lds) {
+  bf16_t* qa = reinterpret_cast<bf16_t*>(lds + LDS_QA);
+  const int lane = lane_id();
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int dd = 2 * lane + e;
+      const float x = hh == 0 ? (e == 0 ? q0.x : q0.y) : (e == 0 ? q1.x : q1.y);
+      const bf16_t hi = f32_to_bf16(x);
+      const float r1 = x - bf16_to_f32(hi);
+      const bf16_t mid = f32_to_bf16(r1);
+      const bf16_t lo = f32_to_bf16(r1 - bf16_to_f32(mid));
+      const int s = dd >> 5, col = 16 * ((dd & 31) >> 3), el = dd & 7;
+      bf16_t* base = qa + (size_t)(s * 64 + col) * 8 + el;
+      base[(4 * hh + 0) * 8] = hi;
+      base[(4 * hh + 1) * 8] = mid;
+      base[(4 * hh + 2) * 8] = lo;
+    }
+  }
+}
+// All threads: zero LDS_QA (the rows q_operand_store never writes stay zero afterwards).
+MQ_DEV void q_operand_clear(float* lds) {
+  for (int i = tid(); i < 4 * 64 * 4; i += MQ_THREADS) lds[LDS_QA + i] = 0.f;
+}
+
+// Sync-wave prologue of an attention item on the raw q of query heads 2h, 2h+1 and the k and v
+// of kv head h (v[0..3], dims 2 lane, 2 lane + 1 each) and the read-only parameters (q_norm and
+// k_norm weight pairs wq / wk, RoPE row pairs c2 / s2, as bf16x2): per-head RMSNorm + RoPE in
+// registers.  Leaves q-hat of both query heads in LDS_QA (MFMA operand) and ALDS_QS (fp32), the
+// new position's k-hat and v rounded to bf16 (kept as fp32) in ALDS_KN / ALDS_VN, and the new
+// position's two scores (q-hat . bf16 k-hat, log2 domain) in ALDS_SNEW; the compute waves read
+// them after the phase's closing __syncthreads.  The cache row itself is written later by the
+// sync wave (attn_cache_row), so no compute wave ever waits for a store.
+MQ_DEV void attn_prologue(const float2* v, uint32_t wq, uint32_t wk, uint32_t c2, uint32_t s2,
+                          float scale_log2, float* lds) {
+  const int lane = lane_id();
+  const float2 c = make_float2(bf16_lo(c2), bf16_hi(c2));
+  const float2 s = make_float2(bf16_lo(s2), bf16_hi(s2));
+  const float2 wqf = make_float2(bf16_lo(wq), bf16_hi(wq));
+  const float2 q0 = head_norm_rope2(v[0], wqf, c, s);
+  const float2 q1 = head_norm_rope2(v[1], wqf, c, s);
+  const float2 k = head_norm_rope2(v[2], make_float2(bf16_lo(wk), bf16_hi(wk)), c, s);
+  const float2 kb = make_float2(round_bf16(k.x), round_bf16(k.y));
+  const float sn0 = wave_sum(q0.x * kb.x + q0.y * kb.y) * scale_log2;
+  const float sn1 = wave_sum(q1.x * kb.x + q1.y * kb.y) * scale_log2;
+  reinterpret_cast<float2*>(lds + ALDS_QS)[lane] = q0;
+  reinterpret_cast<float2*>(lds + ALDS_QS + MQ_D)[lane] = q1;
+  reinterpret_cast<float2*>(lds + ALDS_KN)[lane] = kb;
+  reinterpret_cast<float2*>(lds + ALDS_VN)[lane] =
+      make_float2(round_bf16(v[3].x), round_bf16(v[3].y));
+  if (lane == 0) reinterpret_cast<float2*>(lds + ALDS_SNEW)[0] = make_float2(sn0, sn1);
+  q_operand_store(q0, q1, lds);
+}
+// Sync-wave input of an attention item of the decode kernels: group h's q|k|v words of the layer
+// (xq, epoch e; the parameters are loaded before the poll, in the same round trip), then the
+// prologue.
+MQ_DEV void attn_input(const uint64_t* xq, uint32_t e, MqSync* sy, const bf16_t* qn,
+                       const bf16_t* kn, const bf16_t* cs, const bf16_t* sn, float scale_log2,
+                       float* lds) {
+  const int lane = lane_id();
+  const uint32_t wq = ld32(qn + 2 * lane), wk = ld32(kn + 2 * lane);
+  const uint32_t c2 = ld32(cs + 2 * lane), s2 = ld32(sn + 2 * lane);
+  float r[8];
+  // word i of this lane: vector i / 2 (q0, q1, k, v of the group's 512 rows), dim 2 lane + i % 2
+  x_poll<8>(xq, [&](int i) { return (i >> 1) * MQ_D + 2 * lane + (i & 1); }, e, sy,
+            [&](int i, float v) { r[i] = v; });
+  float2 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = make_float2(r[2 * i], r[2 * i + 1]);
+  attn_prologue(v, wq, wk, c2, s2, scale_log2, lds);
+}
+// The same from the op-level fp32 q|k|v vector (rows in the fused q|k|v order).
+MQ_DEV void attn_input_f(const float* qkv, const bf16_t* qn, const bf16_t* kn, const bf16_t* cs,
+                         const bf16_t* sn, int h, float scale_log2, float* lds) {
   const int lane = lane_id();
   float2 v[4];
   v[0] = ld_coh2(qkv + 2 * h * MQ_D + 2 * lane);
   v[1] = ld_coh2(qkv + 2 * h * MQ_D + 128 + 2 * lane);
   v[2] = ld_coh2(qkv + MQ_QDIM + h * MQ_D + 2 * lane);
   v[3] = ld_coh2(qkv + MQ_QDIM + MQ_KVDIM + h * MQ_D + 2 * lane);
-  uint32_t prm[4];
-  prm[0] = ld32(qn + 2 * lane);
-  prm[1] = ld32(kn + 2 * lane);
-  prm[2] = ld32(cs + 2 * lane);
-  prm[3] = ld32(sn + 2 * lane);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) reinterpret_cast<float2*>(lds + ALDS_RAW)[lane + 64 * i] = v[i];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    reinterpret_cast<float2*>(lds + ALDS_PRM)[64 * i + lane] =
-        make_float2(bf16_lo(prm[i]), bf16_hi(prm[i]));
-}
-
-// Prologue of an attention item (inputs and parameters in LDS): q-hat of query heads 2h, 2h+1
-// into ALDS_QS; k-hat and v of the new position rounded to bf16 (kept as fp32) into
-// ALDS_KN / ALDS_VN.  Waves 0..3 each own one head.  The cache row itself is written later by
-// the sync wave (attn_cache_row), so no compute wave ever waits for a store.
-MQ_DEV void attn_prologue(float* lds) {
-  const int lane = lane_id(), wave = wave_id();
-  const float* raw = lds + ALDS_RAW;
-  const float* prm = lds + ALDS_PRM;
-  if (wave < 2) {
-    float lo = raw[wave * MQ_D + lane], hi = raw[wave * MQ_D + 64 + lane];
-    head_norm_rope(lo, hi, prm, prm + 256, prm + 384);
-    lds[ALDS_QS + wave * MQ_D + lane] = lo;
-    lds[ALDS_QS + wave * MQ_D + 64 + lane] = hi;
-  } else if (wave == 2) {
-    float lo = raw[256 + lane], hi = raw[256 + 64 + lane];
-    head_norm_rope(lo, hi, prm + 128, prm + 256, prm + 384);
-    lds[ALDS_KN + lane] = round_bf16(lo);
-    lds[ALDS_KN + 64 + lane] = round_bf16(hi);
-  } else if (wave == 3) {
-    lds[ALDS_VN + lane] = round_bf16(raw[384 + lane]);
-    lds[ALDS_VN + 64 + lane] = round_bf16(raw[384 + 64 + lane]);
-  }
+  const uint32_t wq = ld32(qn + 2 * lane), wk = ld32(kn + 2 * lane);
+  const uint32_t c2 = ld32(cs + 2 * lane), s2 = ld32(sn + 2 * lane);
+  attn_prologue(v, wq, wk, c2, s2, scale_log2, lds);
 }
 
 // Sync wave: the new position's K and V rows (bf16) into the cache of `layer`, kv head h.  The
@@ -344,219 +435,226 @@ MQ_DEV void attn_cache_row(const MqDecodeParams& p, int layer, int h, int pos, c
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// K/V of up to MQ_ATT_BLOCK positions: position blk + k*28 + wave*4 + (lane/16) goes to compute
-// wave `wave`, row lane/16, each lane holding 8 of the 128 dims (16 bytes).
-//
+// A block of up to MQ_ATT_BLOCK (224) cache positions of an attention item: position
+// blk + w + 7 i is the i-th position (i < 32) of compute wave w.
+//   K, in the B-operand order of v_mfma_f32_16x16x32_bf16 (lane l: column l % 16, k-dims
+//   8 (l / 16) .. + 8 of a 32-dim step): k[g][s] holds dims 32 s + 8 (lane / 16) .. + 8 of the
+//   wave's position 16 g + lane % 16;
+//   V: v[i] holds dims 2 lane, 2 lane + 1 of the wave's position i (one 256-byte row per wave
+//   load).
 // The row of the position being decoded (pos_new) is never loaded: it is written during this
-// step (attn_cache_row) and its values come from LDS instead.  Fetching it before the write would
-// leave a stale copy in this CU's L1 and this XCD's L2, and a chained launch reads the row with
-// plain loads in the next step.  Every row below pos_new was written by an earlier step (of this
-// launch, with device-scope stores ordered by the barriers in between, or of an earlier kernel)
-// and was not loaded by anyone before that write, so a plain load of it cannot hit a stale line.
+// step (attn_cache_row) and enters the softmax from LDS instead (ALDS_SNEW / ALDS_VN).  Fetching
+// it before the write would leave a stale copy in this CU's L1 and this XCD's L2, and a chained
+// launch reads the row with plain loads in the next step.  Every row below pos_new was written by
+// an earlier step (of this launch, with device-scope stores ordered by the barriers in between,
+// or of an earlier kernel) and was not loaded by anyone before that write, so a plain load of it
+// cannot hit a stale line.
+#define MQ_ATT_PER_WAVE (MQ_ATT_BLOCK / MQ_CWAVES)
+static_assert(MQ_ATT_PER_WAVE == 32, "two 16-position MFMA column groups per compute wave");
 struct KvBlock {
-  uint4 k[MQ_ATT_NK], v[MQ_ATT_NK];
+  uint4 k[2][4];
+  uint32_t v[MQ_ATT_PER_WAVE];
 };
-MQ_DEV void kv_block_load(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int blk, int bend,
-                          int pos_new, bool small = false) {
-  const int lane = lane_id(), wave = wave_id();
-  // small chunks (<= 28 positions): wave 0 holds position blk + 4k + row in slot k
-  if (wave >= (small ? 1 : MQ_CWAVES)) return;
-#pragma unroll
-  for (int k = 0; k < MQ_ATT_NK; ++k) {
-    const int pp = small ? blk + k * 4 + (lane >> 4)
-                         : blk + k * 4 * MQ_CWAVES + wave * 4 + (lane >> 4);
-    if (pp < bend && pp != pos_new && (!small || k < MQ_ATT_SLOT / 4)) {
-      b.k[k] = ld16(Kb + (size_t)pp * MQ_D);
-      b.v[k] = ld16(Vb + (size_t)pp * MQ_D);
-    } else {
-      b.k[k] = b.v[k] = make_uint4(0, 0, 0, 0);
-    }
-  }
+MQ_DEV const bf16_t* kv_base(const bf16_t* cache, const MqDecodeParams& p, int layer, int h) {
+  return cache + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
 }
-// Same block with a fixed instruction count: every compute wave issues all 2 * MQ_ATT_NK loads.
-// Lanes whose position is past bend or is pos_new read the read-only row `dummy` (16 bytes per
-// lane of a 256-byte row) instead, so no unwritten cache row is fetched; attn_core masks the
-// former and replaces the latter from LDS.  Used for the early prefetch of long contexts, where
-// the compiler must know how many loads follow the q|k|v weights to wait for those alone.
-template <bool K, bool V>
-MQ_DEV void kv_block_load_all(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int blk, int bend,
-                              int pos_new, const bf16_t* dummy) {
+MQ_DEV int att_pos(int blk, int wave, int i) { return blk + wave + MQ_CWAVES * i; }
+// Positions [blk, bend) of the wave that exist: i < n_i (wave-uniform).
+MQ_DEV int att_count(int blk, int bend, int wave) {
+  return __builtin_amdgcn_readfirstlane(
+      min(MQ_ATT_PER_WAVE, max(0, (bend - blk - wave + MQ_CWAVES - 1) / MQ_CWAVES)));
+}
+// K rows of a block.  FIXED issues every load (positions past bend or equal to pos_new read the
+// read-only 256-byte row `dummy` instead), so the compiler knows how many loads follow earlier
+// ones; otherwise groups past bend are skipped and their registers zeroed.
+template <bool FIXED>
+MQ_DEV void kv_load_k(KvBlock& b, const bf16_t* Kb, int blk, int bend, int pos_new,
+                      const bf16_t* dummy) {
   const int lane = lane_id(), wave = wave_id();
   if (wave >= MQ_CWAVES) return;
+  const int n = att_count(blk, bend, wave);
 #pragma unroll
-  for (int k = 0; k < MQ_ATT_NK; ++k) {
-    const int pp = blk + k * 4 * MQ_CWAVES + wave * 4 + (lane >> 4);
-    const bool row = pp < bend && pp != pos_new;
-    if constexpr (K) b.k[k] = ld16(row ? Kb + (size_t)pp * MQ_D : dummy);
-    if constexpr (V) b.v[k] = ld16(row ? Vb + (size_t)pp * MQ_D : dummy);
+  for (int g = 0; g < 2; ++g) {
+    if (!FIXED && 16 * g >= n) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b.k[g][s] = make_uint4(0, 0, 0, 0);
+      continue;
+    }
+    const int pp = att_pos(blk, wave, 16 * g + (lane & 15));
+    const bf16_t* row = (pp < bend && pp != pos_new ? Kb + (size_t)pp * MQ_D : dummy) +
+                        8 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) b.k[g][s] = ld16(row + 32 * s);
   }
 }
-MQ_DEV const bf16_t* kv_base(const bf16_t* cache, const MqDecodeParams& p, int layer, int h) {
-  return cache + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D + (lane_id() & 15) * 8;
+template <bool FIXED>
+MQ_DEV void kv_load_v(KvBlock& b, const bf16_t* Vb, int blk, int bend, int pos_new,
+                      const bf16_t* dummy) {
+  const int lane = lane_id(), wave = wave_id();
+  if (wave >= MQ_CWAVES) return;
+  const int n = att_count(blk, bend, wave);
+#pragma unroll
+  for (int i = 0; i < MQ_ATT_PER_WAVE; ++i) {
+    if (!FIXED && i >= n) {
+      b.v[i] = 0;
+      continue;
+    }
+    const int pp = att_pos(blk, wave, i);
+    b.v[i] = ld32((pp < bend && pp != pos_new ? Vb + (size_t)pp * MQ_D : dummy) + 2 * lane);
+  }
+}
+template <bool FIXED>
+MQ_DEV void kv_block_load(KvBlock& b, const bf16_t* Kb, const bf16_t* Vb, int blk, int bend,
+                          int pos_new, const bf16_t* dummy) {
+  kv_load_k<FIXED>(b, Kb, blk, bend, pos_new, dummy);
+  kv_load_v<FIXED>(b, Vb, blk, bend, pos_new, dummy);
 }
 
-// Core of one attention item: kv head h, cache positions [p0, p1), first block already in `b`.
-// Rotated queries in ALDS_QS; position `pos_new` (if inside the range) takes its K/V from
-// ALDS_KN/ALDS_VN instead of the cache.  Each compute wave runs its own online softmax over its
-// positions (4 per wave-instruction: 16 lanes x 8 dims, DPP row sums), keeping scores, running
-// max, sum and p * V in registers; one merge over the waves at the end.  Leaves m[2], l[2] in
-// ALDS_STAT and the unnormalised o[2][128] in ALDS_ORED[0..255] (reference:
-// fused_decode_ldg_common.inl:417-602).
+typedef __bf16 mq_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float mq_f32x4_t __attribute__((ext_vector_type(4)));
+MQ_DEV mq_bf16x8_t bf16x8_of(uint4 v) { return __builtin_bit_cast(mq_bf16x8_t, v); }
+
+// Attention output of a single chunk covering every position: o / l as the log-sum-exp merge
+// computes it for one partial (weight exp2(m - m) / l = 1 / l, then one fused multiply), so the
+// persistent kernel's local result and the one-kernel-per-phase merge of the published partial
+// are bitwise equal.
+MQ_DEV float att_single(float o, float l) { return fmaf(1.0f / l, o, 0.f); }
+
+// Core of one attention item (reference: fused_decode_ldg_common.inl:417-602): query heads 2h,
+// 2h + 1 over cache positions [p0, p1) of kv head h, first block already in `b`, q-hat in LDS_QA;
+// with `has_new` the item also holds the position being decoded, whose score and bf16 v come
+// from ALDS_SNEW / ALDS_VN (its cache row is never read).  Per compute wave and block:
+//   scores on MFMA: S^T[q-part][position] = A (three bf16 parts per query head) x K^T, summed
+//   over the parts: lanes 0-15 hold head 0's scores of the 16 positions of a column group,
+//   lanes 16-31 head 1's;
+//   online softmax per wave (DPP row max / sum over the 16 lanes of a head), weights through
+//   the wave's LDS slice;
+//   p . V on VALU: lane l accumulates dims 2l, 2l + 1 of both heads over the wave's positions,
+//   so no cross-lane reduction is needed.
+// Then one log-sum-exp merge over the waves (and the new position) by 256 threads, leaving
+// m[2], l[2] in ALDS_STAT and the unnormalised o[2][128] in ALDS_ORED[0..255], or with `to_att`
+// (an item over every position) the attention output o / l in LDS_ATTH.
 MQ_DEV void attn_core(const MqDecodeParams& p, int layer, int h, int p0, int p1, int pos_new,
-                      KvBlock& b, float* lds, bool small = false) {
-  const float* qs = lds + ALDS_QS;
-  const float* kn = lds + ALDS_KN;
-  const float* vn = lds + ALDS_VN;
+                      bool has_new, KvBlock& b, float* lds, bool to_att = false) {
   float* wml = lds + ALDS_WML;
   float* stat = lds + ALDS_STAT;
   float* ored = lds + ALDS_ORED;
   const int lane = lane_id(), wave = wave_id();
-  const int g = lane >> 4, sub = lane & 15;
-  // small chunks (<= 28 positions, one block): wave 0 alone takes every position, slot k holding
-  // position blk + 4k + row, and the merge below has a single wave to combine
-  const int nwaves = small ? 1 : MQ_CWAVES;
-  if (wave < nwaves) {
+  if (wave < MQ_CWAVES) {
     const bf16_t* Kb = kv_base(p.kc, p, layer, h);
     const bf16_t* Vb = kv_base(p.vc, p, layer, h);
-    float q0[8], q1[8];
+    const bf16_t* dummy = p.cos;
+    const uint4* qa = reinterpret_cast<const uint4*>(lds + LDS_QA);
+    mq_bf16x8_t a[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      q0[e] = qs[sub * 8 + e];
-      q1[e] = qs[MQ_D + sub * 8 + e];
-    }
-    float acc0[8], acc1[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc0[e] = acc1[e] = 0.f;
-    float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;   // l: this lane's row only
+    for (int s = 0; s < 4; ++s) a[s] = bf16x8_of(qa[s * 64 + lane]);
+    float* pw = lds + ALDS_WSC + wave * 64;      // this wave's weights [i][head]
+    const bool lead = lane < 32;                 // lanes holding scores (head lane / 16)
+    float m = -INFINITY, lsum = 0.f;             // per head (lanes 0-15 / 16-31)
+    float acc00 = 0.f, acc01 = 0.f, acc10 = 0.f, acc11 = 0.f;   // [head][dim 2 lane + e]
     for (int blk = p0; blk < p1; blk += MQ_ATT_BLOCK) {
-      // keeps the next block's loads from being hoisted into this one (two blocks would not
-      // fit in registers)
+      // keeps the next block's loads from being hoisted into this one
       asm volatile("" ::: "memory");
       const int bend = min(p1, blk + MQ_ATT_BLOCK);
-      if (blk != p0) kv_block_load(b, Kb, Vb, blk, bend, pos_new);
-      if (pos_new >= blk && pos_new < bend) {
-        // the new position is not in the cache yet: its bf16 K/V (exact as bf16) replace the
-        // registers of the lane row that holds it
-        const uint4 knp = pack8_bf16(kn + sub * 8), vnp = pack8_bf16(vn + sub * 8);
+      if (blk != p0) kv_block_load<false>(b, Kb, Vb, blk, bend, pos_new, dummy);
+      const int n = att_count(blk, bend, wave);
+      float sc[2];
 #pragma unroll
-        for (int k = 0; k < MQ_ATT_NK; ++k) {
-          if ((small ? blk + k * 4 + g : blk + k * 4 * MQ_CWAVES + wave * 4 + g) == pos_new) {
-            b.k[k] = knp;
-            b.v[k] = vnp;
+      for (int g = 0; g < 2; ++g) {
+        sc[g] = -INFINITY;
+        if (16 * g < n) {
+          mq_f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s], bf16x8_of(b.k[g][s]), c, 0, 0, 0);
+          const float sv = ((c[0] + c[1]) + c[2]) * p.scale_log2;
+          const int pp = att_pos(blk, wave, 16 * g + (lane & 15));
+          sc[g] = lead && pp < bend && pp != pos_new ? sv : -INFINITY;
+        }
+      }
+      const float n_m = fmaxf(m, row16_max(fmaxf(sc[0], sc[1])));
+      const bool empty = n_m == -INFINITY;      // no position of this head so far
+      const float al = empty ? 1.f : exp2_fast(m - n_m);
+      const float w0 = empty ? 0.f : exp2_fast(sc[0] - n_m);
+      const float w1 = empty ? 0.f : exp2_fast(sc[1] - n_m);
+      lsum = fmaf(lsum, al, row16_sum(w0 + w1));
+      m = n_m;
+      if (lead) {
+        pw[(lane & 15) * 2 + (lane >> 4)] = w0;
+        pw[(16 + (lane & 15)) * 2 + (lane >> 4)] = w1;
+      }
+      // rescale by each head's factor (lane 0: head 0, lane 16: head 1)
+      const float al0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al), 0));
+      const float al1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al), 16));
+      acc00 *= al0;
+      acc01 *= al0;
+      acc10 *= al1;
+      acc11 *= al1;
+      // in runs of 8 positions (a data-dependent exit inside the unrolled loop kept the block out
+      // of registers); weights past n are 0
+#pragma unroll
+      for (int q8 = 0; q8 < MQ_ATT_PER_WAVE / 8; ++q8) {
+        if (8 * q8 < n) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int i = 8 * q8 + e;
+            const float2 w = reinterpret_cast<const float2*>(pw)[i];
+            const float v0 = bf16_lo(b.v[i]), v1 = bf16_hi(b.v[i]);
+            acc00 = fmaf(w.x, v0, acc00);
+            acc01 = fmaf(w.x, v1, acc01);
+            acc10 = fmaf(w.y, v0, acc10);
+            acc11 = fmaf(w.y, v1, acc11);
           }
         }
       }
-      // scores of this wave's 32 positions, (head, k * 4 + row), in its own LDS slice
-      float* wsc = lds + ALDS_WSC + wave * 64;
-      float mx0 = -INFINITY, mx1 = -INFINITY;
-      // position slots k of this wave holding at least one position below bend (wave-uniform)
-      const int nk = small ? (bend - blk + 3) / 4
-                           : min(MQ_ATT_NK, max(0, (bend - blk - wave * 4 + 4 * MQ_CWAVES - 1) /
-                                                      (4 * MQ_CWAVES)));
-#pragma unroll
-      for (int k = 0; k < MQ_ATT_NK; ++k) {
-        if (k >= nk) break;
-        const int pp = small ? blk + k * 4 + g : blk + k * 4 * MQ_CWAVES + wave * 4 + g;
-        float kv[8];
-        unpack8(b.k[k], kv);
-        float d0 = 0.f, d1 = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          d0 = fmaf(q0[e], kv[e], d0);
-          d1 = fmaf(q1[e], kv[e], d1);
-        }
-        d0 = pp < bend ? row16_sum(d0) * p.scale_log2 : -INFINITY;
-        d1 = pp < bend ? row16_sum(d1) * p.scale_log2 : -INFINITY;
-        if (sub == 0) {
-          wsc[k * 4 + g] = d0;
-          wsc[32 + k * 4 + g] = d1;
-        }
-        mx0 = fmaxf(mx0, d0);
-        mx1 = fmaxf(mx1, d1);
-      }
-      mx0 = max_xor32(max_xor16(mx0));
-      mx1 = max_xor32(max_xor16(mx1));
-      const float n0 = fmaxf(m0, mx0), n1 = fmaxf(m1, mx1);
-      // rescale of what this wave accumulated so far (nothing yet while its max is -inf)
-      const float al0 = n0 == -INFINITY ? 1.f : exp2_fast(m0 - n0);
-      const float al1 = n1 == -INFINITY ? 1.f : exp2_fast(m1 - n1);
-      l0 *= al0;
-      l1 *= al1;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        acc0[e] *= al0;
-        acc1[e] *= al1;
-      }
-#pragma unroll
-      for (int k = 0; k < MQ_ATT_NK; ++k) {
-        if (k >= nk) break;
-        const int pp = small ? blk + k * 4 + g : blk + k * 4 * MQ_CWAVES + wave * 4 + g;
-        const float w0 = pp < bend ? exp2_fast(wsc[k * 4 + g] - n0) : 0.f;
-        const float w1 = pp < bend ? exp2_fast(wsc[32 + k * 4 + g] - n1) : 0.f;
-        l0 += w0;
-        l1 += w1;
-        float vv[8];
-        unpack8(b.v[k], vv);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          acc0[e] = fmaf(w0, vv[e], acc0[e]);
-          acc1[e] = fmaf(w1, vv[e], acc1[e]);
-        }
-      }
-      m0 = n0;
-      m1 = n1;
     }
-    // sum the wave's 4 position rows (lane groups of 16 share the wave's max) with row swaps,
-    // so that the merge below reads one row per wave
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      acc0[e] = sum_xor32(sum_xor16(acc0[e]));
-      acc1[e] = sum_xor32(sum_xor16(acc1[e]));
-    }
-    l0 = sum_xor32(sum_xor16(l0));
-    l1 = sum_xor32(sum_xor16(l1));
-    if (g == 0) {
-      float4* arow = reinterpret_cast<float4*>(lds + LDS_AROW + wave * 256 + sub * 8);
-      arow[0] = make_float4(acc0[0], acc0[1], acc0[2], acc0[3]);
-      arow[1] = make_float4(acc0[4], acc0[5], acc0[6], acc0[7]);
-      arow[MQ_D / 4] = make_float4(acc1[0], acc1[1], acc1[2], acc1[3]);
-      arow[MQ_D / 4 + 1] = make_float4(acc1[4], acc1[5], acc1[6], acc1[7]);
-    }
-    if (lane == 0) {
-      wml[wave * 4 + 0] = m0;
-      wml[wave * 4 + 1] = m1;
-      lds[LDS_AL + wave * 2 + 0] = l0;
-      lds[LDS_AL + wave * 2 + 1] = l1;
+    float* arow = lds + LDS_AROW + wave * 256;
+    reinterpret_cast<float2*>(arow)[lane] = make_float2(acc00, acc01);
+    reinterpret_cast<float2*>(arow + MQ_D)[lane] = make_float2(acc10, acc11);
+    if ((lane & 15) == 0 && lead) {
+      wml[wave * 4 + (lane >> 4)] = m;
+      wml[wave * 4 + 2 + (lane >> 4)] = lsum;
     }
   }
   __syncthreads();
-  // merge the compute waves (every item has at least one valid position, so M is finite); all
-  // LDS reads are issued up front, waves past nwaves are masked by selects (their LDS is stale)
+  // merge the compute waves (waves without a position have m = -inf and weigh 0) and the new
+  // position; every item has at least one position, so M is finite.  All LDS reads first.
   if (tid() < 256) {
-    const int j = tid() >> 7;
+    const int j = tid() >> 7, d = tid() & 127;
     float mw[MQ_CWAVES], ow[MQ_CWAVES], lw[MQ_CWAVES];
 #pragma unroll
     for (int w8 = 0; w8 < MQ_CWAVES; ++w8) {
       mw[w8] = wml[w8 * 4 + j];
       ow[w8] = lds[LDS_AROW + w8 * 256 + tid()];
-      lw[w8] = lds[LDS_AL + w8 * 2 + j];
+      lw[w8] = wml[w8 * 4 + 2 + j];
     }
-    float M = -INFINITY;
+    const float sn = lds[ALDS_SNEW + j], vn = lds[ALDS_VN + d];
+    float M = has_new ? sn : -INFINITY;
 #pragma unroll
-    for (int w8 = 0; w8 < MQ_CWAVES; ++w8)
-      if (w8 < nwaves) M = fmaxf(M, mw[w8]);
+    for (int w8 = 0; w8 < MQ_CWAVES; ++w8) M = fmaxf(M, mw[w8]);
     float o = 0.f, L = 0.f;
 #pragma unroll
     for (int w8 = 0; w8 < MQ_CWAVES; ++w8) {
-      const bool use = w8 < nwaves && mw[w8] != -INFINITY;
+      const bool use = mw[w8] != -INFINITY;
       const float f = use ? exp2_fast(mw[w8] - M) : 0.f;
       o = use ? fmaf(f, ow[w8], o) : o;
       L = use ? fmaf(f, lw[w8], L) : L;
     }
-    ored[tid()] = o;
-    if ((tid() & 127) == 0) {
-      stat[j] = M;
-      stat[2 + j] = L;
+    if (has_new) {
+      const float f = exp2_fast(sn - M);
+      o = fmaf(f, vn, o);
+      L += f;
+    }
+    if (to_att) {
+      // a single chunk over every position: the attention output itself (att_single, as the
+      // one-kernel-per-phase merge computes it from this chunk's published partial)
+      lds[LDS_ATTH + tid()] = att_single(o, L);
+    } else {
+      ored[tid()] = o;
+      if (d == 0) {
+        stat[j] = M;
+        stat[2 + j] = L;
+      }
     }
   }
   __syncthreads();
@@ -694,8 +792,20 @@ MQ_DEV void gu_run(const GateUpSet& ws, const MqLayerW& w, int wg, int G, float*
   }, 2 * nr, lds + LDS_XN, [&](int it, float v) { lds[LDS_PR + it] = v; });
 }
 // Sync-wave epilogue: m = silu(g) * u with silu(x) = x / (1 + e^-x)
-// (fused_decode_ldg_mlp.inl:120-175, fused_decode_ldg_common.inl:123-125).
+// (fused_decode_ldg_mlp.inl:120-175, fused_decode_ldg_common.inl:123-125), published to every
+// group's copy of m [MQ_GROUPS][MQ_I] (passed by a counter barrier).
 MQ_DEV void gu_publish(float* m, int wg, int G, const float* lds) {
+  int r0, nr;
+  row_range(MQ_I, wg, G, r0, nr);
+  for (int t = lane_id(); t < nr; t += 64) {
+    const float gv = lds[LDS_PR + t], uv = lds[LDS_PR + nr + t];
+    const float v = gv / (1.0f + expf(-gv)) * uv;
+#pragma unroll
+    for (int c = 0; c < MQ_GROUPS; ++c) st_coh(m + (size_t)c * MQ_I + r0 + t, v);
+  }
+}
+// The op-level form (fp32 array, plain coherent stores).
+MQ_DEV void gu_publish_f(float* m, int wg, int G, const float* lds) {
   int r0, nr;
   row_range(MQ_I, wg, G, r0, nr);
   for (int t = lane_id(); t < nr; t += 64) {
@@ -705,15 +815,23 @@ MQ_DEV void gu_publish(float* m, int wg, int G, const float* lds) {
 }
 
 // ----------------------------------------------------------------------------- P5: down
+// Hidden rows of workgroup wg for the down projection and the layer output: whole row pairs, so
+// that a pair of bf16 outputs is one exchange word (hidden_publish).
+MQ_DEV void hid_rows(int wg, int G, int& r0, int& nr) {
+  int p0, np;
+  row_range(MQ_H / 2, wg, G, p0, np);
+  r0 = 2 * p0;
+  nr = 2 * np;
+}
 MQ_DEV void down_load(DownSet& ws, const MqLayerW& w, int wg, int G) {
   int r0, nr;
-  row_range(MQ_H, wg, G, r0, nr);
+  hid_rows(wg, G, r0, nr);
   ws.load([&](int i) { return w.wd + (size_t)(r0 + i) * MQ_I; }, nr);
 }
 // Input: m in LDS_IN; segment dot products -> LDS_PR.
 MQ_DEV void down_run(const DownSet& ws, const MqLayerW& w, int wg, int G, float* lds) {
   int r0, nr;
-  row_range(MQ_H, wg, G, r0, nr);
+  hid_rows(wg, G, r0, nr);
   ws.compute([&](int i) { return w.wd + (size_t)(r0 + i) * MQ_I; }, nr, lds + LDS_IN,
              [&](int it, float v) { lds[LDS_PR + it] = v; });
 }
@@ -722,7 +840,7 @@ MQ_DEV void down_run(const DownSet& ws, const MqLayerW& w, int wg, int G, float*
 template <class Out>
 MQ_DEV void down_publish(int wg, int G, const float* lds, float& res, Out out) {
   int r0, nr;
-  row_range(MQ_H, wg, G, r0, nr);
+  hid_rows(wg, G, r0, nr);
   const int t = lane_id();
   if (t < nr) {
     res = round_bf16((lds[LDS_PR + 2 * t] + lds[LDS_PR + 2 * t + 1]) + res);
@@ -739,7 +857,8 @@ MQ_DEV void down_publish(int wg, int G, const float* lds, float& res, Out out) {
 // from waiting for the first to return; no cache-wide fences are used.
 MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int* tok_out,
                         float* logits, int pos, bool advance_pos, bool round_norm = false,
-                        bool publish_epoch = false, uint32_t step_epoch = 0) {
+                        bool publish_epoch = false, uint32_t step_epoch = 0,
+                        uint32_t xep_next = 0) {
   float* xn = lds + LDS_XN;
   uint64_t* keys = reinterpret_cast<uint64_t*>(lds + LDS_KEYS);
   norm_1024(lds + LDS_IN, p.final_norm, xn, lds + LDS_RED, round_norm);
@@ -780,35 +899,45 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
   }
   if (lane == 0) keys[wave] = best;
   __syncthreads();
-  if (tid() == 0) {
-    uint64_t k = keys[0];
-#pragma unroll
-    for (int i = 1; i < MQ_WAVES; ++i) k = u64_max(k, keys[i]);
+  if (wave == 0) {
     MqSync* sy = &p.st->sync;
-    __hip_atomic_fetch_max(&sy->argmax.v, (unsigned long long)k, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    wait_all_memory();
-    const uint32_t old =
-        __hip_atomic_fetch_add(&sy->done.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == (uint32_t)G - 1) {
-      const unsigned long long kk =
-          __hip_atomic_load(&sy->argmax.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // device-scope store: the next step of a multi-step launch reads it in other workgroups
-      __hip_atomic_store(reinterpret_cast<uint32_t*>(tok_out), argmax_key_index(kk),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&sy->argmax.v, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int i = 0; i < MQ_BAR_STRIPES; ++i)
-        __hip_atomic_store(&sy->bar[i].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int i = 0; i < MQ_NKV; ++i)
-        __hip_atomic_store(&sy->attn[i].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (advance_pos)
-        __hip_atomic_store(&p.st->pos.v, (uint32_t)(pos + 1), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&sy->done.v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t old = 0;
+    if (lane == 0) {
+      uint64_t k = keys[0];
+#pragma unroll
+      for (int i = 1; i < MQ_WAVES; ++i) k = u64_max(k, keys[i]);
+      __hip_atomic_fetch_max(&sy->argmax.v, (unsigned long long)k, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      wait_all_memory();
+      old = __hip_atomic_fetch_add(&sy->done.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (__builtin_amdgcn_readlane(old, 0) == (uint32_t)G - 1) {
+      // the last workgroup: token, then the step's sync state cleared by the whole wave
+      for (int i = lane; i < MQ_BAR_COPIES * MQ_BAR_STRIPES; i += 64)
+        __hip_atomic_store(&sy->bar[i / MQ_BAR_STRIPES][i % MQ_BAR_STRIPES].v, 0u,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane < MQ_NKV)
+        __hip_atomic_store(&sy->attn[lane].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) {
+        const unsigned long long kk =
+            __hip_atomic_load(&sy->argmax.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // device-scope store: the next step of a multi-step launch reads it in other workgroups
+        __hip_atomic_store(reinterpret_cast<uint32_t*>(tok_out), argmax_key_index(kk),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&sy->argmax.v, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (advance_pos)
+          __hip_atomic_store(&p.st->pos.v, (uint32_t)(pos + 1), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        if (xep_next != 0)
+          __hip_atomic_store(&p.st->xep.v, xep_next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&sy->done.v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       if (publish_epoch) {
         // every reset above and the token are complete before the epoch releases the next step
         wait_all_memory();
-        __hip_atomic_store(&p.st->steps.v, step_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0)
+          __hip_atomic_store(&p.st->steps.v, step_epoch, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
@@ -830,8 +959,9 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
 // That is 3 grid-wide and 2 group-local barriers per layer.  For short contexts (cache length
 // <= attn_local_max) steps 2-3 collapse: every workgroup of the group attends over all
 // positions itself (its O rows prefetched with the K/V rows), and the merge barrier goes away.
-// Measured at 1 and 64 positions this wins; at 129 positions the longer attention of every
-// workgroup costs more than the barrier it saves (1404 against 1464 tok/s).
+// Measured per layer (MFMA scores, epoch-word exchanges): at 128 positions local mode takes
+// 18.7 us against 19.2 us split; at 200 positions 19.7 against 19.6, so the default switches
+// to split chunks above 176 positions.
 
 // Local row i of group h's 512 q|k|v rows -> row of the fused q|k|v projection.
 MQ_DEV int grp_row(int h, int i) {
@@ -852,10 +982,12 @@ MQ_DEV void gqkv_run(const QkvSet& ws, const MqLayerW& w, int h, int j, int NG, 
   ws.compute([&](int i) { return qkv_row(w, grp_row(h, r0 + i)); }, nr, lds + LDS_XN,
              [&](int it, float v) { lds[LDS_PR + it] = v; });
 }
-MQ_DEV void gqkv_publish(float* qkv, int h, int j, int NG, const float* lds) {
+// Sync-wave epilogue: this workgroup's rows of group h's q|k|v as (value, epoch e) words into
+// xq [4 * MQ_D] (the group's local row order, grp_row).
+MQ_DEV void gqkv_publish(uint64_t* xq, uint32_t e, int j, int NG, const float* lds) {
   int r0, nr;
   row_range(4 * MQ_D, j, NG, r0, nr);
-  for (int t = lane_id(); t < nr; t += 64) st_coh(qkv + grp_row(h, r0 + t), lds[LDS_PR + t]);
+  for (int t = lane_id(); t < nr; t += 64) st_coh64(xq + r0 + t, xword(lds[LDS_PR + t], e));
 }
 
 // Position chunks of a group: as many chunks of at least one register slot (28 positions) as
@@ -866,7 +998,8 @@ MQ_DEV void gqkv_publish(float* qkv, int h, int j, int NG, const float* lds) {
 // it as the only partial.  Either way the K/V cache row is written by workgroup 0 (has_pos).
 struct GAttn {
   int nch, p0, p1;
-  bool active, has_pos, small, local;
+  bool active, has_pos, has_new, local;   // has_pos: writes the new K/V row; has_new: the
+                                          // chunk holds the new position
 };
 MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos, int local_max, bool all_local) {
   GAttn g;
@@ -877,7 +1010,7 @@ MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos, int local_max, bo
     g.p1 = cache_len;
     g.active = all_local || j == 0;
     g.has_pos = j == 0;
-    g.small = cache_len <= 8;
+    g.has_new = g.active;
     return g;
   }
   const int want = (cache_len + MQ_ATT_SLOT - 1) / MQ_ATT_SLOT;
@@ -888,25 +1021,8 @@ MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos, int local_max, bo
   g.p1 = min(cache_len, g.p0 + clen);
   g.active = j < g.nch;
   g.has_pos = g.active && pos >= g.p0 && pos < g.p1;
-  // one wave has no other wave to hide its dependent reduction steps: it wins only for chunks of
-  // at most two position slots (measured 1.5 against 2.0 us at 4 positions, 3.5 against 2.2 at 28)
-  g.small = clen <= 8;
+  g.has_new = g.has_pos;
   return g;
-}
-// Attention output of a single chunk covering every position: o / l as the log-sum-exp merge
-// computes it for one partial (weight exp2(m - m) / l = 1 / l, then one fused multiply), so the
-// persistent kernel's local result and the one-kernel-per-phase merge of the published partial
-// are bitwise equal.
-MQ_DEV float att_single(float o, float l) { return fmaf(1.0f / l, o, 0.f); }
-// All threads, local mode: attention output of query heads 2h, 2h+1 from attn_core's LDS
-// result (ALDS_ORED, ALDS_STAT) into LDS_ATTH; ends with __syncthreads.
-MQ_DEV void attn_local_out(float* lds) {
-  const int t = tid();
-  float o = 0.f;
-  if (t < 2 * MQ_D) o = att_single(lds[ALDS_ORED + t], lds[ALDS_STAT + 2 + (t >> 7)]);
-  __syncthreads();
-  if (t < 2 * MQ_D) lds[LDS_ATTH + t] = o;
-  __syncthreads();
 }
 // Same from the single published partial of kv head h (one kernel per phase, local mode).
 MQ_DEV void group_single(const float* part, int h, float* lds) {
@@ -999,10 +1115,15 @@ MQ_DEV void opart_run(const OPairSet& ws, const MqLayerW& w, int h, int j, int N
   ws.compute([&](int i) { return opart_row(w, h, r0 + i); }, nr, lds + LDS_ATTH,
              [&](int i, float v) { lds[LDS_PR + i] = v; });
 }
+// opart: MqExchange.opart [MQ_GROUPS copies][MQ_NKV][MQ_H]; each value goes to every copy.
 MQ_DEV void opart_publish(float* opart, int h, int j, int NG, const float* lds) {
   int r0, nr;
   row_range(MQ_H, j, NG, r0, nr);
-  for (int t = lane_id(); t < nr; t += 64) st_coh(opart + h * MQ_H + r0 + t, lds[LDS_PR + t]);
+  for (int t = lane_id(); t < nr; t += 64) {
+    const float v = lds[LDS_PR + t];
+#pragma unroll
+    for (int c = 0; c < MQ_GROUPS; ++c) st_coh(opart + (c * MQ_NKV + h) * MQ_H + r0 + t, v);
+  }
 }
 // a = x + sum_h opart_h, summed in head order (the single-row form for the multi-kernel mode).
 MQ_DEV float a_elem(float x, const float* opart, int r) {
@@ -1056,17 +1177,15 @@ MQ_DEV void gu_input_all(const float* opart, float* lds) {
   }
   __syncthreads();
 }
-// Sync wave: the layer input into LDS_IN and LDS_HID (coherent fp32, or the bf16 embedding row).
-MQ_DEV void input_hidden_coh(float* lds, const float* src) {
+// Sync wave: a layer output (MQ_H / 2 pair words of `src`, epoch e) into LDS dst (and dst2).
+MQ_DEV void hidden_gather(float* dst, float* dst2, const uint64_t* src, uint32_t e, MqSync* sy) {
   const int lane = lane_id();
-  float2 v[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = ld_coh2(src + 2 * (lane + 64 * i));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    reinterpret_cast<float2*>(lds + LDS_IN)[lane + 64 * i] = v[i];
-    reinterpret_cast<float2*>(lds + LDS_HID)[lane + 64 * i] = v[i];
-  }
+  x_poll<MQ_H / 128>(src, [&](int i) { return lane + 64 * i; }, e, sy, [&](int i, float v) {
+    const uint32_t u = __float_as_uint(v);
+    const float2 f = make_float2(bf16_to_f32((bf16_t)(u & 0xffffu)), bf16_to_f32((bf16_t)(u >> 16)));
+    reinterpret_cast<float2*>(dst)[lane + 64 * i] = f;
+    if (dst2 != nullptr) reinterpret_cast<float2*>(dst2)[lane + 64 * i] = f;
+  });
 }
 MQ_DEV void input_hidden_bf16(float* lds, const bf16_t* src) {
   wave_copy_bf16_1024(lds + LDS_IN, src);
@@ -1079,12 +1198,14 @@ MQ_DEV void input_hidden_bf16(float* lds, const bf16_t* src) {
 // first-in first-out in practice, so arriving before the prefetch is issued keeps the arrival
 // from waiting behind tens of KB of weight loads, and the prefetch drains while the barrier
 // completes.
-template <class Epi, class Arrive, class Prefetch, class Wait, class Input>
+// ACK = false (an exchange of epoch words, no counter arrival): the sync wave does not wait for
+// its stores to be acknowledged; readers recognise the words by their epoch.
+template <bool ACK = true, class Epi, class Arrive, class Prefetch, class Wait, class Input>
 MQ_DEV void phase_step(Epi epilogue, Arrive arrive, Prefetch prefetch, Wait wait, Input input) {
   __syncthreads();
   if (wave_id() == MQ_SYNC_WAVE) {
     epilogue();
-    wait_all_memory();
+    if constexpr (ACK) wait_all_memory();
     arrive();
   }
   __syncthreads();
@@ -1115,9 +1236,26 @@ MQ_DEV bool step_inputs(const MqDecodeParams& p, const int* tok_in, int& pos, in
   return true;
 }
 
-MQ_DEV void hidden_out(const MqDecodeParams& p, int l, int r, float v) {
-  st_coh(p.s->hidden + r, v);
-  if (p.trace != nullptr) p.trace[(size_t)l * MQ_H + r] = v;
+// Sync wave, after down_publish: lane t < nr holds the bf16-valued layer output of row r0 + t
+// (r0, nr even).  Each row pair goes as one exchange word (bf16 of row 2k in bits 0-15, of row
+// 2k + 1 in bits 16-31, epoch e in bits 32-63) to every group's copy of the layer's buffer
+// [MQ_H / 2 words]; the rows also go to the debug trace.
+MQ_DEV void hidden_publish(const MqDecodeParams& p, int l, int r0, int nr, float res,
+                           uint32_t e) {
+  const int t = lane_id();
+  const float other = __shfl_xor(res, 1);
+  if (t < nr && (t & 1) == 0) {
+    const uint64_t w = ((uint64_t)e << 32) | (uint64_t)((uint32_t)f32_to_bf16(other) << 16) |
+                       (uint64_t)f32_to_bf16(res);
+#pragma unroll
+    for (int c = 0; c < MQ_GROUPS; ++c) st_coh64(&p.x->h[l & 1][c][(r0 + t) >> 1], w);
+  }
+  if (p.trace != nullptr && t < nr) p.trace[(size_t)l * MQ_H + r0 + t] = res;
+}
+// Row r of a layer-output buffer copy (any epoch).
+MQ_DEV float hidden_row(const uint64_t* src, int r) {
+  const uint32_t u = (uint32_t)ld_coh64(src + (r >> 1));
+  return bf16_to_f32((bf16_t)((r & 1) ? (u >> 16) : (u & 0xffffu)));
 }
 
 MQ_DEV void stamp(const MqDecodeParams& p, int wg, int l, int k) {
@@ -1188,17 +1326,23 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     const int nw = p.num_layers * (int)(sizeof(MqLayerW) / 4);
     for (int i = tid(); i < nw; i += MQ_THREADS)
       reinterpret_cast<uint32_t*>(s_layers)[i] = reinterpret_cast<const uint32_t*>(p.layers)[i];
+    q_operand_clear(lds);
     __syncthreads();
   }
   const int h = wg % MQ_GROUPS, j = wg / MQ_GROUPS, NG = G / MQ_GROUPS;
   MqSync* sy = &p.st->sync;
   MqScratch* s = p.s;
+  MqExchange* x = p.x;
+  const int copy = wg % MQ_GROUPS;        // the exchange copy this workgroup reads
   int r0h, nrh;
-  row_range(MQ_H, wg, G, r0h, nrh);
-  // the step-done epoch before this launch: read by every workgroup before any can complete the
-  // first step (completion needs every workgroup's arrival at the LM head)
+  hid_rows(wg, G, r0h, nrh);
+  // the step-done epoch and the exchange epoch base before this launch: read by every workgroup
+  // before any can complete the first step (completion needs every workgroup's arrival at the
+  // LM head, where the last one advances them)
   const uint32_t epoch0 = __builtin_amdgcn_readfirstlane(
       __hip_atomic_load(&p.st->steps.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const uint32_t xep0 = __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(&p.st->xep.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   QkvSet wq;
   OPairSet wo;
   GateUpSet wgu;
@@ -1214,68 +1358,62 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
     uint32_t nbar = 0, ngb = 0;
     phase_step(MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
-    // K/V block of this workgroup's chunk (EARLY: row 0 for a workgroup without one)
-    const bool small = EARLY ? false : ga.small;
+    // first K/V block of this workgroup's chunk (EARLY: stand-ins for a workgroup without one)
     const int kv0 = ga.active ? ga.p0 : 0;
-    const int kv1 = ga.active ? min(ga.p1, ga.p0 + MQ_ATT_BLOCK) : 1;
-    // read-only stand-in row for lanes that must not fetch a cache row (row 0 of the cos table)
-    const bf16_t* kv_dummy = p.cos + (lane_id() & 15) * 8;
-    auto k_early = [&](int l) {
-      kv_block_load_all<true, false>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), kv0, kv1,
-                                     pos, kv_dummy);
-    };
+    const int kv1 = ga.active ? min(ga.p1, ga.p0 + MQ_ATT_BLOCK) : 0;
+    // read-only stand-in row for positions that must not fetch a cache row (row 0 of the cos table)
+    const bf16_t* kv_dummy = p.cos;
+    auto k_early = [&](int l) { kv_load_k<true>(kv, kv_base(p.kc, p, l, h), kv0, kv1, pos, kv_dummy); };
     if constexpr (EARLY) {
       if (p.num_layers > 0) k_early(0);
     }
     for (int l = 0; l < p.num_layers; ++l) {
       const MqLayerW w = lds_layer(s_layers, l);
+      const int par = l & 1;
+      // exchange epoch of this step and layer (never 0, never reused: the base only grows)
+      const uint32_t e = xep0 + (uint32_t)(step * p.num_layers + l) + 1u;
       stamp(p, wg, l, 0);
       gqkv_run(wq, w, h, j, NG, lds);
       stamp(p, wg, l, 1);
-      // the gate|up weights go out two phases ahead, during the attention phase, from workgroups
-      // without an attention chunk; the others issue them once they have arrived at the grid
-      // barrier after the O projection (a deep queue stalls the issue of loads and would delay
-      // their attention, the partial merge and the O projection, which are on the critical path).
-      // Workgroups with a chunk issue its K/V rows here instead, after arriving: issued before
+      // q|k|v -> attention: epoch words inside the kv-head group.  The gate|up weights go out two
+      // phases ahead, during the attention phase, from workgroups without an attention chunk;
+      // the others issue them after the O projection (a deep queue stalls the issue of loads and
+      // would delay their attention, the partial merge and the O projection, which are on the
+      // critical path).  Workgroups with a chunk issue its K/V rows here instead: issued before
       // the q|k|v dot products (whose loads are conditional), they made the compiler's wait for
       // the q|k|v weights wait for them too.
-      phase_step([&] { gqkv_publish(s->qkv, h, j, NG, lds); },
-                 [&] { group_barrier_arrive(sy, h); },
-                 [&] {
-                   if constexpr (EARLY) {
-                     // a workgroup without a chunk (some cache lengths below ~990 leave the
-                     // last one idle) takes the gate|up weights here, as in the other variant
-                     if (!ga.active) {
-                       gu_load(wgu, w, wg, G);
-                     } else {
-                       kv_block_load_all<false, true>(kv, kv_base(p.kc, p, l, h),
-                                                      kv_base(p.vc, p, l, h), kv0, kv1, pos,
-                                                      kv_dummy);
-                       if (ga.local) opart_load(wo, w, h, j, NG);
-                     }
-                   } else {
-                     if (!ga.active) {
-                       gu_load(wgu, w, wg, G);
-                     } else {
-                       kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
-                                     min(ga.p1, ga.p0 + MQ_ATT_BLOCK), pos, ga.small);
-                       // local mode: no exchange follows the attention, so the O rows go now
-                       if (ga.local) opart_load(wo, w, h, j, NG);
-                     }
-                   }
-                 },
-                 [&] { group_barrier_wait(sy, h, (++ngb) * (uint32_t)NG); },
-                 [&] { if (ga.active) attn_input(s->qkv, w.q_norm, w.k_norm, cs, sn, h, lds); });
+      phase_step<false>(
+          [&] { gqkv_publish(x->q[par][h], e, j, NG, lds); }, MQ_NOTHING,
+          [&] {
+            if constexpr (EARLY) {
+              // a workgroup without a chunk (some cache lengths below ~990 leave the last one
+              // idle) takes the gate|up weights here, as in the other variant
+              if (!ga.active) {
+                gu_load(wgu, w, wg, G);
+              } else {
+                kv_load_v<true>(kv, kv_base(p.vc, p, l, h), kv0, kv1, pos, kv_dummy);
+                if (ga.local) opart_load(wo, w, h, j, NG);
+              }
+            } else {
+              if (!ga.active) {
+                gu_load(wgu, w, wg, G);
+              } else {
+                kv_block_load<false>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), kv0,
+                                     kv1, pos, kv_dummy);
+                // local mode: no exchange follows the attention, so the O rows go now
+                if (ga.local) opart_load(wo, w, h, j, NG);
+              }
+            }
+          },
+          MQ_NOTHING,
+          [&] {
+            if (ga.active)
+              attn_input(x->q[par][h], e, sy, w.q_norm, w.k_norm, cs, sn, p.scale_log2, lds);
+          });
       stamp(p, wg, l, 2);
-      if (ga.active) {
-        attn_prologue(lds);
-        __syncthreads();
-        attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds, small);
-      }
+      if (ga.active) attn_core(p, l, h, ga.p0, ga.p1, pos, ga.has_new, kv, lds, ga.local);
       stamp(p, wg, l, 3);
-      if (ga.local) {
-        attn_local_out(lds);
-      } else {
+      if (!ga.local) {
         phase_step([&] { if (ga.active) gattn_publish(p, l, pos, h, j, ga, lds); },
                    [&] { group_barrier_arrive(sy, h); },
                    [&] { opart_load(wo, w, h, j, NG); },
@@ -1285,45 +1423,49 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       stamp(p, wg, l, 4);
       opart_run(wo, w, h, j, NG, lds);
       stamp(p, wg, l, 5);
+      // O partials -> a: every group's copy, replicated grid barrier
       phase_step([&] {
-                   opart_publish(&s->opart[0][0], h, j, NG, lds);
+                   opart_publish(&x->opart[0][0][0], h, j, NG, lds);
                    // local mode: the new position's K/V row (ALDS_KN/VN are still intact)
                    if (ga.local && ga.has_pos) attn_cache_row(p, l, h, pos, lds);
                  },
                  [&] { grid_barrier_arrive(sy); },
                  [&] { if (ga.active) gu_load(wgu, w, wg, G); },
                  [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); }, MQ_NOTHING);
-      gu_input_all(&s->opart[0][0], lds);
+      gu_input_all(&x->opart[copy][0][0], lds);
       stamp(p, wg, l, 6);
       gu_run(wgu, w, wg, G, lds);
       stamp(p, wg, l, 7);
-      phase_step([&] { gu_publish(s->mlp, wg, G, lds); },
+      // silu(gate) * up -> down: every group's copy, replicated grid barrier
+      phase_step([&] { gu_publish(&x->m[0][0], wg, G, lds); },
                  [&] { grid_barrier_arrive(sy); },
                  [&] { down_load(wd, w, wg, G); },
                  [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); },
-                 [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, s->mlp); });
+                 [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, x->m[copy]); });
       stamp(p, wg, l, 8);
       down_run(wd, w, wg, G, lds);
       stamp(p, wg, l, 9);
-      phase_step(
+      // layer output -> next layer (or the LM head): epoch words
+      phase_step<false>(
           [&] {
             float res = lane_id() < nrh ? lds[LDS_A + r0h + lane_id()] : 0.f;
-            down_publish(wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); });
+            down_publish(wg, G, lds, res, [](int, float) {});
+            hidden_publish(p, l, r0h, nrh, res, e);
           },
-          [&] { grid_barrier_arrive(sy); },
+          MQ_NOTHING,
           [&] {
             if (l + 1 < p.num_layers) {
               gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG);
               if constexpr (EARLY) k_early(l + 1);
             }
           },
-          [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); },
-          [&] { input_hidden_coh(lds, s->hidden); });
+          MQ_NOTHING, [&] { hidden_gather(lds + LDS_IN, lds + LDS_HID, x->h[par][copy], e, sy); });
       stamp(p, wg, l, 10);
     }
     const bool more = step + 1 < p.nsteps;
     lm_head_run(p, wg, G, lds, p.tok_out + step, p.nsteps == 1 ? p.logits : nullptr, pos, true,
-                false, more, epoch0 + (uint32_t)step + 1);
+                false, more, epoch0 + (uint32_t)step + 1,
+                xep0 + (uint32_t)((step + 1) * p.num_layers));
     if (more) {
       // the next step's first weights do not depend on its token: in flight during the wait
       if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG);
@@ -1342,18 +1484,23 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
   int pos, tok;
   if (!step_inputs(p, p.tok_in, pos, tok)) return;
   MqScratch* s = p.s;
+  MqExchange* x = p.x;
   MqSync* sy = &p.st->sync;
   const int h = wg % MQ_GROUPS, j = wg / MQ_GROUPS, NG = G / MQ_GROUPS;
+  const int par = l & 1;
   const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
+  // exchange words of this mode carry epoch 0: written by a completed earlier kernel, they are
+  // read without waiting (copy 0 of the grid-wide buffers)
+  const uint64_t* xprev = x->h[(l + 1) & 1][0];   // layer l - 1's output
   // the layer input: the embedding row for layer 0, else the previous layer's output
   auto load_x = [&](float* dst) {
     if (l == 0) wave_copy_bf16_1024(dst, xe);
-    else wave_copy_coh<MQ_H>(dst, s->hidden);
+    else hidden_gather(dst, nullptr, xprev, 0, sy);
   };
   if constexpr (PH == 5) {
     phase_sync(sy, 0, false, MQ_NOTHING, [&] {
       if (p.num_layers == 0) wave_copy_bf16_1024(lds + LDS_IN, xe);
-      else wave_copy_coh<MQ_H>(lds + LDS_IN, s->hidden);
+      else hidden_gather(lds + LDS_IN, nullptr, x->h[(p.num_layers - 1) & 1][0], 0, sy);
     });
     lm_head_run(p, wg, G, lds, p.tok_out, p.logits, pos, true);
   } else {
@@ -1363,21 +1510,20 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       gqkv_load(ws, w, h, j, NG);
       phase_sync(sy, 0, false, MQ_NOTHING, [&] { load_x(lds + LDS_IN); });
       gqkv_run(ws, w, h, j, NG, lds);
-      phase_finish([&] { gqkv_publish(s->qkv, h, j, NG, lds); });
+      phase_finish([&] { gqkv_publish(x->q[par][h], 0, j, NG, lds); });
     }
     if constexpr (PH == 1) {
       const GAttn ga = gattn_plan(j, NG, pos + 1, pos, p.attn_local_max, false);
       if (ga.active) {
         KvBlock kv;
-        kv_block_load(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
-                      min(ga.p1, ga.p0 + MQ_ATT_BLOCK), pos, ga.small);
+        kv_block_load<false>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
+                             min(ga.p1, ga.p0 + MQ_ATT_BLOCK), pos, p.cos);
+        q_operand_clear(lds);
         phase_sync(sy, 0, false, MQ_NOTHING, [&] {
-          attn_input(s->qkv, w.q_norm, w.k_norm, p.cos + (size_t)pos * MQ_D,
-                     p.sin + (size_t)pos * MQ_D, h, lds);
+          attn_input(x->q[par][h], 0, sy, w.q_norm, w.k_norm, p.cos + (size_t)pos * MQ_D,
+                     p.sin + (size_t)pos * MQ_D, p.scale_log2, lds);
         });
-        attn_prologue(lds);
-        __syncthreads();
-        attn_core(p, l, h, ga.p0, ga.p1, pos, kv, lds, ga.small);
+        attn_core(p, l, h, ga.p0, ga.p1, pos, ga.has_new, kv, lds);
         phase_finish([&] { gattn_publish(p, l, pos, h, j, ga, lds); });
       }
     }
@@ -1390,7 +1536,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       else
         group_merge(s->part, h, ga.nch, lds);
       opart_run(ws, w, h, j, NG, lds);
-      phase_finish([&] { opart_publish(&s->opart[0][0], h, j, NG, lds); });
+      phase_finish([&] { opart_publish(&x->opart[0][0][0], h, j, NG, lds); });
     }
     if constexpr (PH == 3) {
       GateUpSet ws;
@@ -1398,26 +1544,27 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       phase_sync(sy, 0, false, MQ_NOTHING, [&] {
         load_x(lds + LDS_HID);
         wait_all_memory();
-        gu_input(&s->opart[0][0], lds);
+        gu_input(&x->opart[0][0][0], lds);
       });
       gu_run(ws, w, wg, G, lds);
-      phase_finish([&] { gu_publish(s->mlp, wg, G, lds); });
+      phase_finish([&] { gu_publish(&x->m[0][0], wg, G, lds); });
     }
     if constexpr (PH == 4) {
       DownSet ws;
       down_load(ws, w, wg, G);
       int r0h, nrh;
-      row_range(MQ_H, wg, G, r0h, nrh);
+      hid_rows(wg, G, r0h, nrh);
       const int t = lane_id();
       float res = 0.f;
       if (wave_id() == MQ_SYNC_WAVE && t < nrh) {
-        const float x = l == 0 ? bf16_to_f32(xe[r0h + t]) : ld_coh(s->hidden + r0h + t);
-        res = a_elem(x, &s->opart[0][0], r0h + t);
+        const float xv = l == 0 ? bf16_to_f32(xe[r0h + t]) : hidden_row(xprev, r0h + t);
+        res = a_elem(xv, &x->opart[0][0][0], r0h + t);
       }
-      phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, s->mlp); });
+      phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, x->m[0]); });
       down_run(ws, w, wg, G, lds);
       phase_finish([&] {
-        down_publish(wg, G, lds, res, [&](int r, float v) { hidden_out(p, l, r, v); });
+        down_publish(wg, G, lds, res, [](int, float) {});
+        hidden_publish(p, l, r0h, nrh, res, 0);
       });
     }
   }
@@ -1436,15 +1583,13 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_qkv_kernel(MqDecodeParams p,
 }
 __global__ void __launch_bounds__(MQ_THREADS) mq_op_rope_kernel(MqDecodeParams p, int l, int pos,
                                                                  float* q_out) {
-  __shared__ __align__(16) float lds[ALDS_WML];
+  __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   const int h = blockIdx.x;
   const MqLayerW w = p.layers[l];
   phase_sync(&p.st->sync, 0, false, MQ_NOTHING, [&] {
-    attn_input(p.s->qkv, w.q_norm, w.k_norm, p.cos + (size_t)pos * MQ_D,
-               p.sin + (size_t)pos * MQ_D, h, lds);
+    attn_input_f(p.s->qkv, w.q_norm, w.k_norm, p.cos + (size_t)pos * MQ_D,
+                 p.sin + (size_t)pos * MQ_D, h, p.scale_log2, lds);
   });
-  attn_prologue(lds);
-  __syncthreads();
   if (tid() < 256) q_out[2 * h * MQ_D + tid()] = lds[ALDS_QS + tid()];
   if (wave_id() == MQ_SYNC_WAVE) attn_cache_row(p, l, h, pos, lds);
 }
@@ -1456,11 +1601,17 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_attn_kernel(MqDecodeParams p
   const AttnItem it = attn_item(blockIdx.x, nch, cache_len);
   if (!it.active) return;
   KvBlock kv;
-  kv_block_load(kv, kv_base(p.kc, p, l, it.h), kv_base(p.vc, p, l, it.h), it.p0,
-                min(it.p1, it.p0 + MQ_ATT_BLOCK), -1);
-  if (tid() < 256) lds[ALDS_QS + tid()] = q_hat[2 * it.h * MQ_D + tid()];
+  kv_block_load<false>(kv, kv_base(p.kc, p, l, it.h), kv_base(p.vc, p, l, it.h), it.p0,
+                       min(it.p1, it.p0 + MQ_ATT_BLOCK), -1, p.cos);
+  q_operand_clear(lds);
   __syncthreads();
-  attn_core(p, l, it.h, it.p0, it.p1, -1, kv, lds);
+  if (wave_id() == MQ_SYNC_WAVE) {
+    const float* qh = q_hat + 2 * it.h * MQ_D;
+    q_operand_store(make_float2(qh[2 * lane_id()], qh[2 * lane_id() + 1]),
+                    make_float2(qh[MQ_D + 2 * lane_id()], qh[MQ_D + 2 * lane_id() + 1]), lds);
+  }
+  __syncthreads();
+  attn_core(p, l, it.h, it.p0, it.p1, -1, false, kv, lds);
   attn_write_partial(p.s->part, it.h, it.c, lds);
 }
 __global__ void __launch_bounds__(MQ_THREADS) mq_op_merge_kernel(MqDecodeParams p, int nch,
@@ -1491,7 +1642,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_gateup_kernel(MqDecodeParams
   gu_load(ws, p.layers[l], blockIdx.x, gridDim.x);
   phase_sync(&p.st->sync, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, a); });
   gu_run(ws, p.layers[l], blockIdx.x, gridDim.x, lds);
-  phase_finish([&] { gu_publish(p.s->mlp, blockIdx.x, gridDim.x, lds); });
+  phase_finish([&] { gu_publish_f(p.s->mlp, blockIdx.x, gridDim.x, lds); });
 }
 __global__ void __launch_bounds__(MQ_THREADS) mq_op_down_kernel(MqDecodeParams p, int l,
                                                                  const float* a, bf16_t* x_out) {
@@ -1499,7 +1650,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_down_kernel(MqDecodeParams p
   DownSet ws;
   down_load(ws, p.layers[l], blockIdx.x, gridDim.x);
   int r0, nr;
-  row_range(MQ_H, blockIdx.x, gridDim.x, r0, nr);
+  hid_rows(blockIdx.x, gridDim.x, r0, nr);
   float res = lane_id() < nr ? ld_coh(a + r0 + lane_id()) : 0.f;
   phase_sync(&p.st->sync, 0, false, MQ_NOTHING,
              [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, p.s->mlp); });
@@ -1523,11 +1674,14 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, 
 // ---------------------------------------------------------------------- state kernels
 __global__ void mq_fill_state_kernel(MqState* st, int pos, int clear_err) {
   const int t = threadIdx.x;
-  if (t < MQ_BAR_STRIPES) st->sync.bar[t].v = 0;
+  if (t < MQ_BAR_COPIES * MQ_BAR_STRIPES) st->sync.bar[t / MQ_BAR_STRIPES][t % MQ_BAR_STRIPES].v = 0;
   if (t < MQ_NKV) st->sync.attn[t].v = 0;
   if (t == 0) {
     st->sync.done.v = 0;
-    if (clear_err) st->sync.err.v = 0;
+    if (clear_err) {
+      st->sync.err.v = 0;
+      st->xep.v = 0;
+    }
     st->sync.argmax.v = 0;
     st->pos.v = (uint32_t)pos;
     st->steps.v = 0;
@@ -1601,8 +1755,15 @@ int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t st
 }
 
 int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream, bool clear_err) {
-  mq_fill_state_kernel<<<1, 64, 0, stream>>>(st, pos, clear_err ? 1 : 0);
+  mq_fill_state_kernel<<<1, MQ_BAR_COPIES * MQ_BAR_STRIPES, 0, stream>>>(st, pos,
+                                                                         clear_err ? 1 : 0);
   return launch_status();
+}
+
+int mq_launch_clear_state(MqState* st, MqExchange* x, hipStream_t stream) {
+  const int rc = mq_launch_zero(x, sizeof(MqExchange), stream);
+  if (rc != 0) return rc;
+  return mq_launch_fill_state(st, 0, stream, true);
 }
 
 int mq_launch_zero(void* ptr, size_t bytes, hipStream_t stream) {

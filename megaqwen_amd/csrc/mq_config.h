@@ -24,8 +24,7 @@
                                         // weight-pointer table in LDS)
 #define MQ_STEPS_PER_LAUNCH 64          // decode_steps: tokens chained inside one persistent launch
 #define MQ_PART_STRIDE 132              // floats per attention partial: m, l, pad, pad, o[128]
-#define MQ_ATT_NK 8                     // positions per compute-wave row per attention block
-#define MQ_ATT_BLOCK (4 * MQ_CWAVES * MQ_ATT_NK)   // 224 positions scored per pass of a chunk
-#define MQ_ATT_SLOT (4 * MQ_CWAVES)     // 28 positions: one register slot of every compute wave
-#define MQ_ATT_LOCAL_DEFAULT 64        // default attn_local_max (persistent decode)
+#define MQ_ATT_BLOCK (32 * MQ_CWAVES)   // 224 positions scored per pass of a chunk (32 per wave)
+#define MQ_ATT_SLOT (4 * MQ_CWAVES)     // 28: the smallest split-K chunk (4 positions per wave)
+#define MQ_ATT_LOCAL_DEFAULT 176       // default attn_local_max (persistent decode)
 #define MQ_GROUPS MQ_NKV                // persistent decode: workgroup wg serves kv head wg % 8

@@ -25,23 +25,47 @@ struct MqLayerW {
   const bf16_t* wd;
 };
 
-// fp32 activations of one decode step (lives in the caller's workspace).  Every array here is
-// written and read across workgroups with the coherent (sc1) accessors of mq_device.h.
+// fp32 activations of the op-level entry points and the attention split-K partials (in the
+// caller's workspace).  Every array here is written and read across workgroups with the coherent
+// (sc1) accessors of mq_device.h.
 struct MqScratch {
   float qkv[MQ_QKV];           // raw q | k | v projections (before q/k RMSNorm and RoPE)
   float att[MQ_QDIM];          // merged attention output
   float a[MQ_H];               // residual stream after attention: W_o att + x
   float mlp[MQ_I];             // silu(gate) * up
-  float hidden[MQ_H];          // residual stream at a layer boundary: bf16-rounded values (the
-                               // reference keeps it in bf16, fused_decode_ldg_mlp.inl:200)
   float part[MQ_NKV * MQ_MAX_CHUNKS * MQ_GQA * MQ_PART_STRIDE];  // attention split-K partials
-  float opart[MQ_NKV][MQ_H];   // per-kv-head O-projection partials: W_o[:, head h cols] att_h
 };
+
+// Exchange buffers of the decode kernels (in the caller's workspace).  Values that cross
+// workgroups without a counter barrier travel as 64-bit (value, epoch) words: the low 32 bits are
+// the fp32 value, the high 32 bits the exchange epoch of the step and layer that wrote it.  A
+// reader polls the words it needs until every one carries the epoch it expects: one store and one
+// load per value, no acknowledgement wait before an arrival and no atomic.  The buffers
+// alternate by layer parity.  Values every workgroup reads are written once per kv-head group
+// (copy g is read by the workgroups wg % 8 == g), so each cache line has 32 readers instead of
+// 256; on MI355X that took a 1024-value exchange among 256 workgroups from 3.4 to 1.6 us.
+// The one-kernel-per-phase mode writes the same buffers with epoch 0 (never expected: epochs
+// start at 1) and reads the values only.  The two larger exchanges (the O partials, 8192 values,
+// and silu(gate) * up, 3072) measured no faster as epoch words than with a counter barrier whose
+// counters are replicated per group, and would not fit the sync wave's registers as one poll.
+struct MqExchange {
+  uint64_t q[2][MQ_NKV][4 * MQ_D];       // q|k|v rows of each kv-head group (read by the group)
+  uint64_t h[2][MQ_GROUPS][MQ_H / 2];    // layer output: a bf16 row pair per word (bits 0-15
+                                         // row 2k, 16-31 row 2k + 1), epoch in bits 32-63
+  // passed by counter barriers (fp32, one copy per group):
+  float opart[MQ_GROUPS][MQ_NKV][MQ_H];  // per-kv-head O-projection partials W_o[:, head h] att_h
+  float m[MQ_GROUPS][MQ_I];              // silu(gate) * up
+};
+MQ_DEV uint64_t xword(float v, uint32_t e) { return ((uint64_t)e << 32) | __float_as_uint(v); }
+MQ_DEV float xvalue(uint64_t w) { return __uint_as_float((uint32_t)w); }
+MQ_DEV uint32_t xepoch(uint64_t w) { return (uint32_t)(w >> 32); }
 
 struct MqState {
   MqSync sync;
   MqLine pos;                  // device-side decode position (read at step start, +1 at step end)
   MqLine steps;                // completed steps of multi-step launches (the step-done epoch)
+  MqLine xep;                  // exchange epochs used so far (+num_layers per persistent step);
+                               // only creation and reset, which clear MqExchange, zero it
 };
 
 struct MqDecodeParams {
@@ -62,6 +86,7 @@ struct MqDecodeParams {
   float* trace;                // optional fp32 [num_layers, H]: hidden state after every layer
   uint64_t* stamps;            // optional [grid][num_layers][MQ_NSTAMP] 100 MHz timestamps
   MqScratch* s;
+  MqExchange* x;
   MqState* st;
   float scale_log2;            // log2(e) / sqrt(D): scores are kept in the log2 domain
   int attn_local_max;          // cache lengths up to this are attended over all positions by
@@ -116,6 +141,9 @@ __host__ __device__ inline int mq_decode_early_kv(int pos, int grid, int local_m
 // (sticky until mq_decoder_reset or creation, so mq_decoder_check still reports it) unless
 // `clear_err`.
 int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream, bool clear_err = false);
+// Creation / reset: the state as above with the error flag and the exchange epoch zeroed, and the
+// exchange buffers cleared (no stale word can carry an epoch a later step expects).
+int mq_launch_clear_state(MqState* st, MqExchange* x, hipStream_t stream);
 int mq_launch_zero(void* ptr, size_t bytes, hipStream_t stream);
 int mq_decode_grid(int mode, int* grid_out);
 int mq_read_error(MqState* st, hipStream_t stream, uint32_t* err_out);

@@ -224,6 +224,12 @@ MQ_DEV float2 ld_coh2(const float* p) {
                                        __HIP_MEMORY_SCOPE_AGENT);
   return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
 }
+MQ_DEV uint64_t ld_coh64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+MQ_DEV void st_coh64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 MQ_DEV void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ---------------------------------------------------------------------------- grid barrier
@@ -237,8 +243,11 @@ struct alignas(128) MqLine64 {
   uint32_t pad[30];
 };
 #define MQ_BAR_STRIPES 32
+#define MQ_BAR_COPIES 8
 struct MqSync {
-  MqLine bar[MQ_BAR_STRIPES];  // striped grid-barrier arrival counters (reset at step end)
+  MqLine bar[MQ_BAR_COPIES][MQ_BAR_STRIPES];  // grid-barrier arrival counters: every workgroup
+                               // adds to its stripe of each copy and polls copy wg % 8 (reset at
+                               // step end)
   MqLine attn[MQ_NKV];         // per-kv-head group barrier / split-K completion counters
                                // (reset at step end)
   MqLine done;                 // LM-head completion counter
@@ -260,36 +269,37 @@ MQ_DEV uint32_t row16_sum_u32(uint32_t v) {
 
 // Grid-wide barrier for a co-resident (cooperative) launch, executed by the sync wave only
 // (the caller brackets it with __syncthreads).  `target` is the arrival count that completes
-// this barrier: k * gridDim.x for the k-th barrier of the launch.  Workgroup w arrives on stripe
-// w % 32 (32 counters in separate lines cut the serialisation of 256 atomics on one line: with
-// the 16 counters packed into one line a token took 25% longer, 32 lines measured 0.5-3% faster
-// than 16); lanes 0..31 poll all stripes at once and sum them with DPP.  The sync wave never has weight
-// prefetches outstanding, so its polls are not queued behind them (gfx9 returns a wave's loads
-// in order).  Precondition: the compute waves have waited for the stores other workgroups will
-// read before the __syncthreads that precedes this call.
+// this barrier: k * gridDim.x for the k-th barrier of the step.  Workgroup w adds 1 to stripe
+// w % 32 of each of the 8 counter copies (lanes 0-7, one atomic each; the counters of a copy sit
+// in 32 separate 128-byte lines, since atomics on one line serialise) and lanes 0..31 poll the
+// 32 stripes of copy w % 8 at once and sum them with DPP, so each line is polled by 32
+// workgroups rather than 256 (measured 3.7 against 4.4 us for an 8192-value exchange among 256
+// workgroups).  The sync wave never has weight prefetches outstanding, so its polls are not
+// queued behind them (gfx9 returns a wave's loads in order).  Precondition: the stores other
+// workgroups will read after this barrier have been waited for.
 MQ_DEV void grid_barrier_arrive(MqSync* s) {
-  if (__lane_id() == 0)
-    __hip_atomic_fetch_add(&s->bar[blockIdx.x % MQ_BAR_STRIPES].v, 1u, __ATOMIC_RELAXED,
+  const int lane = __lane_id();
+  if (lane < MQ_BAR_COPIES)
+    __hip_atomic_fetch_add(&s->bar[lane][blockIdx.x % MQ_BAR_STRIPES].v, 1u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
 }
 MQ_DEV void grid_barrier_wait(MqSync* s, uint32_t target) {
   const int lane = __lane_id();
+  const int copy = blockIdx.x % MQ_BAR_COPIES;
   uint32_t spins = 0;
   while (true) {
     uint32_t v = 0;
     // the error flag (one line that every workgroup would poll) is read on every 8th poll only
     if (lane < MQ_BAR_STRIPES)
-      v = __hip_atomic_load(&s->bar[lane].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v = __hip_atomic_load(&s->bar[copy][lane].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else if (lane == 63 && (spins & 7) == 0)
       v = __hip_atomic_load(&s->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t e = __builtin_amdgcn_readlane(v, 63);
     const uint32_t rs = row16_sum_u32(v);
     const uint32_t total = __builtin_amdgcn_readlane(rs, 0) + __builtin_amdgcn_readlane(rs, 16);
     if (e != 0 || (int32_t)(total - target) >= 0) break;
-    // back-off of ~128 clocks between polls: 256 workgroups x 16 lanes polling the stripe lines
-    // back to back slow down the arrivals on those lines (measured 1496-1508 against 1440 tok/s
-    // at pos 128 on one box; 1 to 8 units of s_sleep measure alike, the group barrier's single
-    // poller gains nothing from it)
+    // back-off of ~128 clocks between polls: polling back to back slows down the arrivals on
+    // the stripe lines
     __builtin_amdgcn_s_sleep(2);
     if (++spins > MQ_SPIN_LIMIT) {
       if (lane == 0)
