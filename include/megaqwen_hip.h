@@ -216,6 +216,20 @@ int mq_op_decode_layer(mq_decoder* dec, int layer, const void* d_x_bf16, int pos
 int mq_op_lm_head(mq_decoder* dec, const void* d_x_bf16, int32_t* d_token_out, float* d_logits,
                   void* stream);
 
+/* ---- Unmasked multi-head attention over [B, H, T, 64] (the ASR audio tower's self-attention).
+ * Replaces flash_attn_bhwd (megaqwen/triton_flash_attn.py:27-171); that function's argument
+ * checks (:38-50) are made by its Python front end (megaqwen_amd/flash_attn.py).
+ * out = softmax(scale * q k^T) v for every (batch, head), no mask.  q, k, v, out: contiguous
+ * [batch, heads, seq_len, head_dim] tensors of one 16-bit type `dtype`; head_dim must be 64.
+ * fp32 arithmetic, output rounded to nearest-even in `dtype`.  Needs no decoder.
+ * seq_len == 0 (or batch or heads 0) is a no-op; batch * heads must be <= 65535; out must not
+ * overlap k or v (it may be q). */
+#define MQ_DTYPE_BF16 0
+#define MQ_DTYPE_F16 1
+int mq_flash_attn_bhwd(const void* d_q, const void* d_k, const void* d_v, void* d_out,
+                       int batch, int heads, int seq_len, int head_dim, int dtype, float scale,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmegaqwen_hip.so")
-SOURCES = ["decode.hip", "prefill.hip", "capi.hip"]
+SOURCES = ["decode.hip", "prefill.hip", "flash_attn.hip", "capi.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

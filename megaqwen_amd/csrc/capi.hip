@@ -16,6 +16,7 @@
 
 #include "../../include/megaqwen_hip.h"
 #include "mq_decode.h"
+#include "mq_flash.h"
 #include "mq_prefill.h"
 
 namespace {
@@ -505,6 +506,36 @@ int mq_op_lm_head(mq_decoder* dec, const void* d_x_bf16, int32_t* d_token_out, f
   int rc = mq_launch_op_lm_head(dec->p, static_cast<const bf16_t*>(d_x_bf16), d_token_out,
                                 d_logits, dec->grid, static_cast<hipStream_t>(stream));
   return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%d)", rc);
+}
+
+int mq_flash_attn_bhwd(const void* d_q, const void* d_k, const void* d_v, void* d_out,
+                       int batch, int heads, int seq_len, int head_dim, int dtype, float scale,
+                       void* stream) {
+  if (batch < 0 || heads < 0 || seq_len < 0)
+    return fail(MQ_ERR_INVALID_ARG, "negative size (batch %d, heads %d, seq_len %d)", batch,
+                heads, seq_len);
+  if (head_dim != 64) return fail(MQ_ERR_INVALID_ARG, "Only head_dim=64 supported, got %d", head_dim);
+  if (dtype != MQ_DTYPE_BF16 && dtype != MQ_DTYPE_F16)
+    return fail(MQ_ERR_INVALID_ARG, "dtype %d is neither MQ_DTYPE_BF16 nor MQ_DTYPE_F16", dtype);
+  if (batch == 0 || heads == 0 || seq_len == 0) return MQ_OK;
+  if (d_q == nullptr || d_k == nullptr || d_v == nullptr || d_out == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "NULL argument");
+  if ((long long)batch * heads > 65535)
+    return fail(MQ_ERR_INVALID_ARG, "batch * heads = %lld exceeds 65535",
+                (long long)batch * heads);
+  const size_t bytes = (size_t)batch * heads * seq_len * head_dim * 2;
+  auto overlaps = [&](const void* a, const void* b) {
+    const char* x = static_cast<const char*>(a);
+    const char* y = static_cast<const char*>(b);
+    return x < y + bytes && y < x + bytes;
+  };
+  if (overlaps(d_out, d_k) || overlaps(d_out, d_v))
+    return fail(MQ_ERR_INVALID_ARG, "out must not overlap k or v");
+  const float scale_log2 = (float)((double)scale * 1.4426950408889634);
+  const int rc = mq_launch_flash_attn_bhwd(d_q, d_k, d_v, d_out, batch * heads, seq_len,
+                                           dtype == MQ_DTYPE_F16, scale_log2,
+                                           static_cast<hipStream_t>(stream));
+  return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%s)", hipGetErrorString(hipGetLastError()));
 }
 
 }  // extern "C"

@@ -24,3 +24,11 @@ PREFILL_2L = 4e-2
 # prefill logits, 28 layers, 512 tokens (seed 0 weights, tokens of seed 1): spread 3.66e-2
 PREFILL_28L_SPREAD = 3.66e-2
 PREFILL_28L = 7e-2
+
+# flash_attn_bhwd (tests/test_gpu_flash_attn.py): the output is the 16-bit rounding of an fp32
+# evaluation, so it must lie within half a unit in the last place of the float64 oracle plus the
+# fp32 evaluation's own error.  That error is bounded by the P hi + lo split (2^-18 of max|v| for
+# bf16, 2^-22 for fp16) plus fp32 accumulation over <= 1500 keys (~2^-24 * sqrt(T)): ~5e-6 of
+# max|v|, held here at 2e-5 of max|v|.  (The reference's Triton kernel evaluates q k^T and P V
+# with TF32 dots, ~1e-3 relative; this bound is tighter than the reference's own accuracy.)
+FLASH_ATTN_ABS = 2e-5
