@@ -161,6 +161,145 @@ def time_prefill(dec, n: int, reps: int):
     return min(times), sum(times) / len(times)
 
 
+QKV_BYTES = 4096 * 1024 * 2 + 1024 * 2 + 2 * 128 * 2        # q|k|v rows, input norm, q/k norms
+MLP_BYTES = 3 * 3072 * 1024 * 2 + 1024 * 2                  # gate, up, down, post-attention norm
+LM_HEAD_BYTES = 151936 * 1024 * 2 + 1024 * 2                # tied LM head, final norm
+ATT_LENGTHS = (1, 128, 1024, 8192, 32768)
+
+
+def time_op(fn, reps: int):
+    """Mean seconds per call of fn() over `reps` calls, and how it was timed.  The calls are
+    captured into one HIP graph and replayed between HIP events, so the figure is device time
+    (kernels and the gaps between them), not the Python/ctypes cost of issuing each call; if
+    capture fails, the calls are issued eagerly between the events instead ("eager")."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / 1e3 / reps, "graph"
+    except RuntimeError:
+        torch.cuda.synchronize()
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / 1e3 / reps, "eager"
+
+
+def time_ops(dec):
+    """each decode op of the Qwen3-0.6B shapes through its C-ABI entry point,
+    as GB/s of its algorithmic bytes against the 8 TB/s HBM peak; plus flash_attn_bhwd (the audio
+    tower's attention, B=1, 14 heads, T=1500) as TFLOP/s against the dense MFMA peak."""
+    import torch
+    from megaqwen_amd.flash_attn import flash_attn_bhwd
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = (torch.randn(1024, device="cuda", generator=g) * 0.5).to(torch.bfloat16)
+    a = torch.randn(1024, device="cuda", generator=g)
+    q = torch.randn(16 * 128, device="cuda", generator=g)
+    qo = torch.empty(16 * 128, device="cuda")
+    xo = torch.empty(1024, dtype=torch.bfloat16, device="cuda")
+    tok = torch.empty(1, dtype=torch.int32, device="cuda")
+    ops = {}
+
+    def entry(name, timed, nbytes):
+        sec, how = timed
+        ops[name] = {"us": round(sec * 1e6, 2), "bytes": int(nbytes),
+                     "gb_s": round(nbytes / sec / 1e9, 1), "frac": round(nbytes / sec / HBM_PEAK, 4),
+                     "timing": how}
+
+    dec.reset()
+    entry("qkv_norm_rope", time_op(lambda: dec.op_qkv_rope(0, x, 100, qo), 200), QKV_BYTES)
+    entry("mlp_swiglu", time_op(lambda: dec.op_mlp(0, a, xo), 200), MLP_BYTES)
+    entry("lm_head_argmax", time_op(lambda: dec.op_lm_head(x, tok), 50), LM_HEAD_BYTES)
+    # K/V ~ N(0, 1) in layer 0's cache rows [0, max(L))
+    n = max(ATT_LENGTHS)
+    dec.k_cache[0, :, :n].normal_(generator=g)
+    dec.v_cache[0, :, :n].normal_(generator=g)
+    for L in ATT_LENGTHS:
+        entry(f"attention_L{L}", time_op(lambda: dec.op_attention(0, q, L, qo), 100),
+              L * 8 * 128 * 2 * 2 + 16 * 128 * 4)
+    qf, kf, vf = (torch.randn(1, 14, 1500, 64, device="cuda", generator=g).to(torch.bfloat16)
+                  for _ in range(3))
+    sec, how = time_op(lambda: flash_attn_bhwd(qf, kf, vf), 50)
+    flops = 4.0 * 14 * 1500 * 1500 * 64
+    ops["flash_attn_bhwd_T1500"] = {"us": round(sec * 1e6, 2), "tflops": round(flops / sec / 1e12, 1),
+                                    "frac_mfma_peak": round(flops / sec / MFMA_BF16_PEAK, 4),
+                                    "timing": how}
+    dec.reset()
+    return ops
+
+
+def time_buckets(dec):
+    """16-token random prompt, greedy decode from position 16 to 256 as one
+    device-side token chain, one persistent launch per bucket (16-63, 64-127, 128-191, 192-255)
+    with an event pair around each.  Returns {bucket: tok/s} and the whole run's wall tok/s."""
+    import torch
+    from megaqwen_amd.synthetic import make_tokens
+    dec.reset()
+    first = dec.prefill_step(make_tokens(16, 151936, seed=0))
+    buckets = [(16, 64), (64, 128), (128, 192), (192, 256)]
+    buf = torch.empty(257, dtype=torch.int32, device="cuda")
+    buf[16] = first
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in buckets]
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for (lo, hi), (a, b) in zip(buckets, ev):
+        a.record(stream)
+        rc = dec._lib.mq_decode_steps(dec._h, buf.data_ptr() + 4 * lo, hi - lo, stream.cuda_stream)
+        b.record(stream)
+        if rc != 0:
+            raise RuntimeError(dec._lib.mq_last_error().decode())
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dec.check()
+    out = {}
+    for (lo, hi), (a, b) in zip(buckets, ev):
+        sec = a.elapsed_time(b) / 1e3
+        mid = (lo + hi - 1) // 2
+        out[f"{lo}-{hi - 1}"] = {"tok_s": round((hi - lo) / sec, 1),
+                                 "roofline_frac": round(bytes_per_token(mid) * (hi - lo) / sec / HBM_PEAK, 4)}
+    return out, round(240 / wall, 1)
+
+
+def write_maps(path: str):
+    """Copies /proc/self/maps (which file is mapped at which address) to `path`."""
+    with open("/proc/self/maps") as src, open(path, "w") as dst:
+        dst.write(src.read())
+
+
+def teardown(*objs):
+    """Ends the run's GPU work before the interpreter exits: waits for the device, drops the
+    decoders and device tensors, and returns the caching allocator's blocks, so nothing of this
+    program is left to be torn down by exit handlers after a profiler tool has finalized."""
+    import gc
+    import torch
+    torch.cuda.synchronize()
+    for o in objs:
+        del o
+    gc.collect()
+    torch.cuda.empty_cache()
+    torch.cuda.synchronize()
+
+
 def pmc_workload():
     """Fixed short run for counter passes (rocprofv3 --pmc ...): every dispatch is profiled, so
     it stays small.  The 256 MiB copy is the calibration kernel for the traffic counters."""
@@ -177,7 +316,10 @@ def pmc_workload():
     toks = dec.decode_steps_cuda(tok, 16)          # one persistent launch of 16 chained tokens
     torch.cuda.synchronize()
     dec.check()
-    print(f"pmc workload done: 256 MiB copy, prefill 128, decode 16 -> {toks[-1].item()}")
+    last = toks[-1].item()
+    del a, b, toks, dec
+    teardown()
+    print(f"pmc workload done: 256 MiB copy, prefill 128, decode 16 -> {last}")
 
 
 def prefill_workload(n: int):
@@ -191,6 +333,8 @@ def prefill_workload(n: int):
     tok = dec.prefill_step(toks)
     torch.cuda.synchronize()
     dec.check()
+    del dec
+    teardown()
     print(f"prefill workload done: 2 x prefill {n} -> {tok}")
 
 
@@ -243,7 +387,13 @@ def main():
                          "decode launch of 16 chained steps at positions 128..143")
     ap.add_argument("--prefill-workload", type=int, default=0, metavar="N",
                     help="for counter runs of the prefill kernels: two N-token prefills, nothing else")
+    ap.add_argument("--maps-out", default="", metavar="PATH",
+                    help="write this process's /proc/self/maps to PATH when the run is done (to "
+                         "attribute addresses in a crash report printed at exit)")
     args = ap.parse_args()
+    if args.maps_out:
+        import atexit
+        atexit.register(write_maps, args.maps_out)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): the decode and prefill "
               "kernels here are single-GPU; there is no multi-GPU path", file=sys.stderr)
@@ -258,7 +408,7 @@ def main():
         return
     K, W = int(args.steps), int(args.warmup)
     positions = (1, 128, 4096)
-    max_seq = positions[-1] + K + 8
+    max_seq = max(positions[-1] + K + 8, max(ATT_LENGTHS))
     dec, spec = build_decoder(max_seq, max_prefill=4096)
     dec.set_mode(args.mode)
     print(f"[bench] decoder ready: mode={dec.mode} grid={dec.grid} max_seq={max_seq}", file=sys.stderr,
@@ -288,6 +438,12 @@ def main():
     print(f"[bench] pos 128, one launch per token: {one_launch['tok_s']} tok/s, kernel "
           f"{one_launch['kernel_us']} us", file=sys.stderr, flush=True)
 
+    buckets, buckets_wall = time_buckets(dec)
+    print(f"[bench] positions 16..255 by bucket: {buckets} (wall {buckets_wall} tok/s)",
+          file=sys.stderr, flush=True)
+    ops = time_ops(dec)
+    print(f"[bench] ops: {ops}", file=sys.stderr, flush=True)
+
     pf_best, pf_mean = time_prefill(dec, 512, 5)
     pf4_best, _ = time_prefill(dec, 4096, 2)
     prefill = {"tokens": 512, "ms": round(pf_mean * 1e3, 3), "tok_s": round(512 / pf_mean, 1),
@@ -303,9 +459,9 @@ def main():
     achieved = head["bytes_per_token"] * head["tokens_per_launch"] / (head["launch_us"] * 1e-6)
     traffic = measured_traffic() if args.mode == "persistent" else None
     cpu = None
+    del dec
+    teardown()
     if not args.no_cpu_baseline:
-        del dec
-        torch.cuda.empty_cache()
         cpu = cpu_baseline()
         print(f"[bench] cpu baseline {cpu['value']:.2f} tok/s on {cpu['cores']} threads",
               file=sys.stderr, flush=True)
@@ -330,6 +486,8 @@ def main():
                                                  for p, r in res.items()},
                    "tokens_per_launch": head["tokens_per_launch"],
                    "tok_s_one_launch_per_token": one_launch,
+                   "tok_s_by_bucket_16_256": buckets, "tok_s_16_256_wall": buckets_wall,
+                   "ops": ops,
                    "prefill": prefill},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 2), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
