@@ -338,6 +338,22 @@ def prefill_workload(n: int):
     print(f"prefill workload done: 2 x prefill {n} -> {tok}")
 
 
+def flash_workload():
+    """For counter runs of flash_attn_bhwd: B = 1, 14 heads, T = 1500, bf16, 10 calls."""
+    import torch
+    from megaqwen_amd.flash_attn import flash_attn_bhwd
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q, k, v = (torch.randn(1, 14, 1500, 64, device="cuda", generator=g).to(torch.bfloat16)
+               for _ in range(3))
+    for _ in range(10):
+        out = flash_attn_bhwd(q, k, v)
+    torch.cuda.synchronize()
+    checksum = float(out.float().abs().sum())
+    del q, k, v, out
+    teardown()
+    print(f"flash workload done: 10 x flash_attn_bhwd [1, 14, 1500, 64] bf16 -> {checksum:.3f}")
+
+
 def cpu_baseline(prompt_len: int = 16, gen: int = 32):
     import torch
     from megaqwen_amd.rope import build_rope_tables
@@ -387,6 +403,8 @@ def main():
                          "decode launch of 16 chained steps at positions 128..143")
     ap.add_argument("--prefill-workload", type=int, default=0, metavar="N",
                     help="for counter runs of the prefill kernels: two N-token prefills, nothing else")
+    ap.add_argument("--flash-workload", action="store_true",
+                    help="for counter runs of flash_attn_bhwd: 10 calls at [1, 14, 1500, 64] bf16")
     ap.add_argument("--maps-out", default="", metavar="PATH",
                     help="write this process's /proc/self/maps to PATH when the run is done (to "
                          "attribute addresses in a crash report printed at exit)")
@@ -405,6 +423,9 @@ def main():
         return
     if args.prefill_workload > 0:
         prefill_workload(args.prefill_workload)
+        return
+    if args.flash_workload:
+        flash_workload()
         return
     K, W = int(args.steps), int(args.warmup)
     positions = (1, 128, 4096)

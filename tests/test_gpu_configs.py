@@ -1,7 +1,8 @@
 """The BASELINE configurations at their real 28-layer shape, checked against the CPU oracle.
 
-- config 3: 16-token prompt, greedy decode from position 16 to 256 (local attention below 64
-  cached positions, split-K attention with the group merge above);
+- config 3: 16-token prompt, greedy decode from position 16 to 256 (local attention up to 176
+  cached positions, the default MEGAQWEN_ATTN_LOCAL_MAX; split-K attention with the group merge
+  above);
 - config 5: 4096-token prefill, then decode at 4096+ on the long-context kernel variant;
 - config 4: 512-token prefill, checked layer by layer through the per-layer trace hook;
 - chained decode (decode_steps_cuda / decode_greedy_cuda, up to 64 tokens per launch) against the
@@ -51,14 +52,14 @@ def full272():
 
 def test_config3_decode_16_to_256_layerwise(full272):
     """16-token random prompt prefilled, then greedy decode from position 16
-    to 255.  Positions up to 63 use the local attention (every workgroup of a kv-head group over
-    all positions); from 64 on the split-K chunks and the group merge run.  Checked layer by
-    layer at positions on both sides of the switch and across the range."""
+    to 255.  Cache lengths up to 176 use the local attention (every workgroup of a kv-head group
+    over all positions); from 177 on the split-K chunks and the group merge run.  Checked layer
+    by layer at positions on both sides of the switch and across the range."""
     dec, orc, sp, _ = full272
     dec.set_mode("persistent")
     dec.reset()
     nxt = dec.prefill_step(make_tokens(16, VOCAB, seed=0))
-    check = {16, 17, 40, 62, 63, 64, 65, 100, 127, 128, 129, 191, 200, 254, 255}
+    check = {16, 17, 40, 63, 64, 100, 127, 128, 174, 175, 176, 177, 191, 200, 254, 255}
     t = nxt
     for pos in range(16, 256):
         if pos in check:
@@ -70,9 +71,9 @@ def test_config3_decode_16_to_256_layerwise(full272):
 
 
 def test_chained_28_layers_across_local_split_and_launch_boundary(full272):
-    """Chained decode from position 0 for 100 tokens at 28 layers: the chain crosses the switch
-    from local to split-K attention (64 positions) inside a launch and the 64-token launch
-    boundary.  Tokens and every KV row equal one launch per token bit for bit; the tokens equal
+    """Chained decode from position 0 for 200 tokens at 28 layers: the chain crosses the switch
+    from local to split-K attention (cache length 177) inside a launch and three 64-token launch
+    boundaries.  Tokens and every KV row equal one launch per token bit for bit; the tokens equal
     the oracle's argmax (teacher-forced on the chain) wherever its margin is above 2 x the
     28-layer logit bound."""
     dec, orc, sp, _ = full272
@@ -80,17 +81,17 @@ def test_chained_28_layers_across_local_split_and_launch_boundary(full272):
     dec.set_mode("persistent")
     dec.reset()
     ref, t = [], first
-    for _ in range(100):
+    for _ in range(200):
         t = dec.decode_step(t)
         ref.append(t)
-    kref, vref = dec.k_cache[:, :, :100].clone(), dec.v_cache[:, :, :100].clone()
+    kref, vref = dec.k_cache[:, :, :200].clone(), dec.v_cache[:, :, :200].clone()
     dec.reset()
-    chain = dec.decode_steps_cuda(first, 100).cpu().tolist()
-    assert chain == ref and dec.position() == 100
-    assert torch.equal(dec.k_cache[:, :, :100], kref)
-    assert torch.equal(dec.v_cache[:, :, :100], vref)
+    chain = dec.decode_steps_cuda(first, 200).cpu().tolist()
+    assert chain == ref and dec.position() == 200
+    assert torch.equal(dec.k_cache[:, :, :200], kref)
+    assert torch.equal(dec.v_cache[:, :, :200], vref)
     orc.reset()
-    _oracle_tokens_agree(orc, first, chain, T.DECODE_28L, "chain 0..99, 28 layers")
+    _oracle_tokens_agree(orc, first, chain, T.DECODE_28L, "chain 0..199, 28 layers")
     dec.check()
 
 
