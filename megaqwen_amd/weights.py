@@ -152,12 +152,16 @@ def load_local_checkpoint(model_dir: Path, max_seq_len: int, device="cuda") -> d
         raise NotImplementedError("quantised (uint8) checkpoints are not supported")
     embed = t[prefix + "embed_tokens.weight"]
     cos, sin = build_rope_tables(max_seq_len, rope_theta, int(spec["head_dim"]))
+    # the tokenizer only from this directory's own files: without them AutoTokenizer can resolve
+    # config.json's model type to a tokenizer found elsewhere, whose ids need not fit this vocab
     tokenizer = None
-    try:
-        from transformers import AutoTokenizer
-        tokenizer = AutoTokenizer.from_pretrained(str(model_dir), local_files_only=True)
-    except Exception:  # a directory without tokenizer files still yields usable weights
-        tokenizer = None
+    if any((model_dir / f).exists() for f in ("tokenizer.json", "tokenizer_config.json",
+                                              "vocab.json")):
+        try:
+            from transformers import AutoTokenizer
+            tokenizer = AutoTokenizer.from_pretrained(str(model_dir), local_files_only=True)
+        except Exception:  # unreadable tokenizer files still leave usable weights
+            tokenizer = None
     out = {
         "embed_weight": embed,
         "layer_weights": [t[f"{prefix}layers.{i}.{s}"] for i in range(n) for s in _LAYER_SUFFIXES],
