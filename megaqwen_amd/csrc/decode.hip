@@ -858,7 +858,7 @@ MQ_DEV void down_publish(int wg, int G, const float* lds, float& res, Out out) {
 MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int* tok_out,
                         float* logits, int pos, bool advance_pos, bool round_norm = false,
                         bool publish_epoch = false, uint32_t step_epoch = 0,
-                        uint32_t xep_next = 0) {
+                        bool set_xep = false, uint32_t xep_next = 0) {
   float* xn = lds + LDS_XN;
   uint64_t* keys = reinterpret_cast<uint64_t*>(lds + LDS_KEYS);
   norm_1024(lds + LDS_IN, p.final_norm, xn, lds + LDS_RED, round_norm);
@@ -928,7 +928,7 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
         if (advance_pos)
           __hip_atomic_store(&p.st->pos.v, (uint32_t)(pos + 1), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
-        if (xep_next != 0)
+        if (set_xep)   // any value, 0 included (the 32-bit epoch count wraps)
           __hip_atomic_store(&p.st->xep.v, xep_next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(&sy->done.v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
@@ -1464,7 +1464,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     }
     const bool more = step + 1 < p.nsteps;
     lm_head_run(p, wg, G, lds, p.tok_out + step, p.nsteps == 1 ? p.logits : nullptr, pos, true,
-                false, more, epoch0 + (uint32_t)step + 1,
+                false, more, epoch0 + (uint32_t)step + 1, true,
                 xep0 + (uint32_t)((step + 1) * p.num_layers));
     if (more) {
       // the next step's first weights do not depend on its token: in flight during the wait
