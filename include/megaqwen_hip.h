@@ -223,12 +223,15 @@ int mq_op_lm_head(mq_decoder* dec, const void* d_x_bf16, int32_t* d_token_out, f
  * [batch, heads, seq_len, head_dim] tensors of one 16-bit type `dtype`; head_dim must be 64.
  * fp32 arithmetic, output rounded to nearest-even in `dtype`.  Needs no decoder.
  * seq_len == 0 (or batch or heads 0) is a no-op; batch * heads must be <= 65535; out must not
- * overlap k or v (it may be q). */
+ * overlap k or v (it may be q).  d_workspace: device memory of at least
+ * mq_flash_attn_workspace_bytes() bytes, 16-byte aligned (K and V^T copies in MFMA-operand
+ * order, written and read within the call). */
 #define MQ_DTYPE_BF16 0
 #define MQ_DTYPE_F16 1
+size_t mq_flash_attn_workspace_bytes(int batch, int heads, int seq_len, int head_dim);
 int mq_flash_attn_bhwd(const void* d_q, const void* d_k, const void* d_v, void* d_out,
                        int batch, int heads, int seq_len, int head_dim, int dtype, float scale,
-                       void* stream);
+                       void* d_workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -30,7 +30,8 @@ EXPORTED = (
     "mq_decoder_create", "mq_decoder_destroy", "mq_decoder_reset", "mq_decoder_position",
     "mq_decoder_set_host_position", "mq_decoder_set_position", "mq_decoder_set_mode", "mq_decoder_get_mode", "mq_decoder_grid", "mq_decode_step",
     "mq_decode_steps", "mq_debug_decode_step_layers", "mq_debug_decode_step_timing", "mq_decoder_check", "mq_prefill", "mq_prefill_embeds", "mq_debug_prefill_layers", "mq_debug_prefill_buffers", "mq_op_qkv_rope", "mq_op_attention", "mq_op_attention_noalloc",
-    "mq_op_mlp", "mq_op_decode_layer", "mq_op_lm_head", "mq_flash_attn_bhwd",
+    "mq_op_mlp", "mq_op_decode_layer", "mq_op_lm_head", "mq_flash_attn_workspace_bytes",
+    "mq_flash_attn_bhwd",
 )
 
 
@@ -99,7 +100,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "mq_op_mlp": (I, [P, I, P, P, P]),
         "mq_op_decode_layer": (I, [P, I, P, I, P, P]),
         "mq_op_lm_head": (I, [P, P, P, P, P]),
-        "mq_flash_attn_bhwd": (I, [P, P, P, P, I, I, I, I, I, ctypes.c_float, P]),
+        "mq_flash_attn_workspace_bytes": (S, [I, I, I, I]),
+        "mq_flash_attn_bhwd": (I, [P, P, P, P, I, I, I, I, I, ctypes.c_float, P, S, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -508,9 +508,22 @@ int mq_op_lm_head(mq_decoder* dec, const void* d_x_bf16, int32_t* d_token_out, f
   return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%d)", rc);
 }
 
+size_t mq_flash_attn_workspace_bytes(int batch, int heads, int seq_len, int head_dim) {
+  if (batch < 0 || heads < 0 || seq_len < 0 || head_dim != 64) {
+    fail(MQ_ERR_INVALID_ARG, "bad shape (batch %d, heads %d, seq_len %d, head_dim %d)", batch,
+         heads, seq_len, head_dim);
+    return 0;
+  }
+  if ((long long)batch * heads > 65535) {
+    fail(MQ_ERR_INVALID_ARG, "batch * heads = %lld exceeds 65535", (long long)batch * heads);
+    return 0;
+  }
+  return mq_flash_attn_workspace(batch * heads, seq_len);
+}
+
 int mq_flash_attn_bhwd(const void* d_q, const void* d_k, const void* d_v, void* d_out,
                        int batch, int heads, int seq_len, int head_dim, int dtype, float scale,
-                       void* stream) {
+                       void* d_workspace, size_t workspace_bytes, void* stream) {
   if (batch < 0 || heads < 0 || seq_len < 0)
     return fail(MQ_ERR_INVALID_ARG, "negative size (batch %d, heads %d, seq_len %d)", batch,
                 heads, seq_len);
@@ -531,9 +544,13 @@ int mq_flash_attn_bhwd(const void* d_q, const void* d_k, const void* d_v, void* 
   };
   if (overlaps(d_out, d_k) || overlaps(d_out, d_v))
     return fail(MQ_ERR_INVALID_ARG, "out must not overlap k or v");
+  const size_t ws = mq_flash_attn_workspace(batch * heads, seq_len);
+  if (d_workspace == nullptr || workspace_bytes < ws || (reinterpret_cast<uintptr_t>(d_workspace) & 15) != 0)
+    return fail(MQ_ERR_INVALID_ARG, "workspace needs %zu bytes, 16-byte aligned (got %zu)", ws,
+                workspace_bytes);
   const float scale_log2 = (float)((double)scale * 1.4426950408889634);
   const int rc = mq_launch_flash_attn_bhwd(d_q, d_k, d_v, d_out, batch * heads, seq_len,
-                                           dtype == MQ_DTYPE_F16, scale_log2,
+                                           dtype == MQ_DTYPE_F16, scale_log2, d_workspace,
                                            static_cast<hipStream_t>(stream));
   return rc == 0 ? MQ_OK : fail(MQ_ERR_HIP, "launch failed (%s)", hipGetErrorString(hipGetLastError()));
 }

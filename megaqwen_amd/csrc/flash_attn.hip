@@ -12,14 +12,17 @@
 //   * K tile row r carries key fa_key_perm(r) (bits 2 and 3 of r swapped).  That makes score
 //     accumulator element j of lane l the key 16 (j / 8) + 8 (l / 32) + j % 8, which is the
 //     B-operand layout of two 16-key MFMA steps: O^T += V^T P^T takes P^T from registers;
-//   * V^T (dims x keys) is formed per tile in a wave-private LDS buffer: a lane loads two key
-//     rows x 16 dims and writes 16 (key, key+1) pairs; the MFMA operand is one 16-byte read;
+//   * K and V^T are first copied (fa_pack_kernel, into the caller's workspace) into per-tile
+//     operand order: each 16-byte operand register of a wave is one contiguous 1 KB load.  Read
+//     from the [T, 64] rows directly, an operand load touches 16-32 cache lines and the loads
+//     bound the kernel;
 //   * the scores are exact fp32 dot products of the 16-bit inputs (up to accumulation order),
 //     the softmax is fp32, and P enters the MFMA as a hi + lo pair of the input type (two
 //     MFMAs), ~16 bits more than one rounding of P; the output is o / l rounded to nearest-even
 //     in the input type (triton_flash_attn.py:126-127).
-// Keys >= T (the last tile) get score -inf and V rows of zero; queries >= T read row T-1 and
-// store nothing.  All loads stay inside [0, T) rows of the tensors.
+// Keys >= T (the last tile) get score -inf and zero V^T entries (the pack writes zeros for
+// them); queries >= T read row T-1 and store nothing.  All loads stay inside the tensors and the
+// workspace.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -32,7 +35,6 @@
 #define FA_QB 32          // queries per workgroup
 #define FA_KT 32          // keys per tile
 #define FA_WAVES 4        // waves per workgroup (split of the key tiles)
-#define FA_VT_PITCH 40    // LDS row pitch of a wave's V^T tile, 16-bit elements (80 bytes)
 #define FA_RESCALE 8.0f   // exponent headroom of the lazily raised softmax reference point
 
 typedef float fa_f32x16 __attribute__((ext_vector_type(16)));
@@ -67,27 +69,51 @@ template <bool F16> MQ_DEV uint32_t fa_pack2(float a, float b) {
   }
 }
 
-// Wave-level ordering point for the wave-private LDS tile: every lane's LDS writes before it
-// are visible to every lane's reads after it, and no LDS access moves across it.
-MQ_DEV void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+// Operand copies of one (batch * head, 32-key tile), 4 KB each, in the workspace:
+//   K' [bh][tile][s 0..3][lane 0..63] (16 bytes): K[32 t + fa_key_perm(lane % 32)][16 s + 8 (lane / 32) ..+8]
+//   V' [bh][tile][2 nt + s][lane] (16 bytes): V[32 t + 16 s + 8 (lane / 32) + e][32 nt + lane % 32], e = 0..7
+// Keys >= T are zero in both.
+__global__ void __launch_bounds__(256) fa_pack_kernel(const uint16_t* __restrict__ k,
+                                                      const uint16_t* __restrict__ v, uint4* kp,
+                                                      uint4* vp, int T, int ntiles) {
+  __shared__ uint16_t sv[FA_KT][FA_D + 8];
+  const int t = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
+  const size_t base = (size_t)bh * T * FA_D;
+  const size_t tile = ((size_t)bh * ntiles + t) * 256;
+  const int lane = tid & 63, s = tid >> 6;
+  {
+    const int key = t * FA_KT + fa_key_perm(lane & 31);
+    kp[tile + tid] = key < T ? ld16(k + base + (size_t)key * FA_D + 16 * s + 8 * (lane >> 5))
+                             : make_uint4(0u, 0u, 0u, 0u);
+  }
+  {
+    const int r = tid >> 3, c = tid & 7, key = t * FA_KT + r;
+    const uint4 w = key < T ? ld16(v + base + (size_t)key * FA_D + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
+    *reinterpret_cast<uint4*>(&sv[r][8 * c]) = w;
+  }
+  __syncthreads();
+  {
+    const int nt = s >> 1, ss = s & 1, dim = 32 * nt + (lane & 31), k0 = 16 * ss + 8 * (lane >> 5);
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = (uint32_t)sv[k0 + 2 * e][dim] | ((uint32_t)sv[k0 + 2 * e + 1][dim] << 16);
+    vp[tile + tid] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
 }
 
 template <bool F16>
 __global__ void __launch_bounds__(64 * FA_WAVES) __attribute__((amdgpu_waves_per_eu(3)))
-fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-               const uint16_t* __restrict__ v, uint16_t* __restrict__ out, int T,
+fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint4* __restrict__ kp,
+               const uint4* __restrict__ vp, uint16_t* __restrict__ out, int T,
                float scale_log2, int nqb, int items, int per_xcd) {
   typedef FaType<F16> Ty;
   typedef typename Ty::v8 v8;
-  // LDS: the workgroup's Q^T operand (shared by its waves, 4 KB) and each wave's V^T tile
-  // during the key loop; the partials of waves 1.. (o: 32 per lane, m, l) afterwards.
+  // LDS: the workgroup's Q^T operand (shared by its waves, 4 KB) during the key loop; the
+  // partials of waves 1.. (o: 32 per lane, m, l) afterwards.
   union FaLds {
     struct {
       uint4 q[4][64];
-      uint16_t vt[FA_WAVES][FA_D * FA_VT_PITCH];
     } loop;
     float red[FA_WAVES - 1][34][64];
   };
@@ -104,12 +130,9 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   const int fr = lane & 31, hh = lane >> 5;
   const size_t base = (size_t)bh * T * FA_D;
   const uint16_t* Q = q + base;
-  const uint16_t* K = k + base;
-  const uint16_t* V = v + base;
   const int qi = qb * FA_QB + fr;                  // this lane's query
   const int ntiles = (T + FA_KT - 1) / FA_KT;
   const int t0 = ntiles * wave / FA_WAVES, t1 = ntiles * (wave + 1) / FA_WAVES;
-  uint16_t* vt = lds.loop.vt[wave];
 
   // Q^T operand in LDS, read by every wave at every tile (registers are the scarcer resource):
   // lds.loop.q[s][lane] = query q0 + lane % 32 (rows >= T read row T-1, never stored), dims
@@ -119,27 +142,19 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     lds.loop.q[wave][lane] = ld16(Q + (size_t)qrow * FA_D + 16 * wave + 8 * hh);
   }
   __syncthreads();
-  // Operands of the key tiles, loaded ahead of their use:
-  //   K operand of tile t: key 32 t + fa_key_perm(fr) (clamped into [0, T)), dims 16 s + 8 hh;
-  //   V rows of tile t held by this lane: keys 32 t + 2 kp, + 1 (clamped into [0, T); the rows
-  //   of keys >= T are zeroed before use, so masked keys contribute 0 * 0), dims 16 dc .. + 16.
-  // The loads are unconditional: a load under a branch makes the compiler wait for every
-  // outstanding load at the next use of any of them.
-  const int kp = lane & 15, dc = lane >> 4;
-  uint4 kr[4], vr[2][2];
+  // Operands of the key tiles from the operand copies, loaded ahead of their use (contiguous
+  // 1 KB per wave instruction).  The loads are unconditional: a load under a branch makes the
+  // compiler wait for every outstanding load at the next use of any of them.
+  const uint4* KP = kp + (size_t)bh * ntiles * 256 + lane;
+  const uint4* VP = vp + (size_t)bh * ntiles * 256 + lane;
+  uint4 kr[4], vr[4];
   auto load_k = [&](int t) {
-    const int key = min(t * FA_KT + fa_key_perm(fr), T - 1);
-    const uint16_t* src = K + (size_t)key * FA_D + 8 * hh;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) kr[s] = ld16(src + 16 * s);
+    for (int s = 0; s < 4; ++s) kr[s] = ld16(KP + (size_t)t * 256 + 64 * s);
   };
   auto load_v = [&](int t) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint16_t* src = V + (size_t)min(t * FA_KT + 2 * kp + i, T - 1) * FA_D + 16 * dc;
-      vr[i][0] = ld16(src);
-      vr[i][1] = ld16(src + 8);
-    }
+    for (int i = 0; i < 4; ++i) vr[i] = ld16(VP + (size_t)t * 256 + 64 * i);
   };
   // S^T of the tile whose K operand is in kr
   auto scores = [&]() {
@@ -166,33 +181,15 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   const bool cpos = scale_log2 >= 0.f;
 
   // Software pipeline: the MFMAs of tile t + 1's scores are issued before tile t's softmax, so
-  // they run while the softmax's VALU work issues, and tile t's V^T is written to LDS first so
-  // that its registers take the next tile's rows a full step before their use.  The last
-  // iteration recomputes its own tile's scores (unused) rather than branch.
+  // they run while the softmax's VALU work issues, and the next tiles' operands are loaded a full
+  // step before their use.  The last iteration recomputes its own tile's scores (unused) rather
+  // than branch.
   auto step = [&](int t, fa_f32x16& sv, fa_f32x16& snext) {
     snext = scores();
     // keys >= T exist only in the row's last tile
     const bool masked = t == ntiles - 1 && T % FA_KT != 0;
-    if (masked) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        if (t * FA_KT + 2 * kp + i >= T) vr[i][0] = vr[i][1] = make_uint4(0u, 0u, 0u, 0u);
-    }
-    // this tile's V^T into the wave's LDS buffer: word (key 2 kp, key 2 kp + 1) of each dim
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t xa[4] = {vr[0][h].x, vr[0][h].y, vr[0][h].z, vr[0][h].w};
-      const uint32_t ya[4] = {vr[1][h].x, vr[1][h].y, vr[1][h].z, vr[1][h].w};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int d = 16 * dc + 8 * h + 2 * c;
-        *reinterpret_cast<uint32_t*>(vt + d * FA_VT_PITCH + 2 * kp) =
-            __builtin_amdgcn_perm(ya[c], xa[c], 0x05040100u);
-        *reinterpret_cast<uint32_t*>(vt + (d + 1) * FA_VT_PITCH + 2 * kp) =
-            __builtin_amdgcn_perm(ya[c], xa[c], 0x07060302u);
-      }
-    }
-    // the next operands: both loads a full step ahead of their use
+    // this tile's V^T operands leave the load registers, which take the next tile's
+    const uint4 vcur[4] = {vr[0], vr[1], vr[2], vr[3]};
     load_k(min(t + 2, t1 - 1));
     load_v(min(t + 1, t1 - 1));
     if (masked) {
@@ -256,7 +253,6 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
 #pragma unroll
         for (int j = 0; j < 16; ++j) o[nt][j] *= alpha;
     }
-    wave_lds_sync();
     // O^T += V^T P^T; V^T operand (nt, s): dim 32 nt + fr, keys 16 s + 8 hh .. + 8
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -264,13 +260,11 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
       const v8 pl = __builtin_bit_cast(v8, make_uint4(plw[4 * s], plw[4 * s + 1], plw[4 * s + 2], plw[4 * s + 3]));
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
-        const v8 vb = __builtin_bit_cast(
-            v8, *reinterpret_cast<const uint4*>(vt + (32 * nt + fr) * FA_VT_PITCH + 16 * s + 8 * hh));
+        const v8 vb = __builtin_bit_cast(v8, vcur[2 * nt + s]);
         o[nt] = Ty::mfma(vb, ph, o[nt]);
         o[nt] = Ty::mfma(vb, pl, o[nt]);
       }
     }
-    wave_lds_sync();
   };
   if (t0 < t1) {
     load_k(t0);
@@ -286,7 +280,7 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
 
   // merge the key ranges in wave order (a wave without tiles has m = -inf and adds 0; at least
   // one wave has a tile, so the common max is finite)
-  __syncthreads();                                 // every wave is done with the loop buffers
+  __syncthreads();                                 // every wave is done with the Q^T operand
   if (wave > 0) {
     float* r = &lds.red[wave - 1][0][lane];
 #pragma unroll
@@ -334,21 +328,30 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   }
 }
 
+size_t mq_flash_attn_workspace(int bh, int T) {
+  return (size_t)2 * bh * ((T + FA_KT - 1) / FA_KT) * FA_KT * FA_D * 2;
+}
+
 int mq_launch_flash_attn_bhwd(const void* q, const void* k, const void* v, void* out, int bh,
-                              int T, bool f16, float scale_log2, hipStream_t stream) {
-  const int nqb = (T + FA_QB - 1) / FA_QB;
+                              int T, bool f16, float scale_log2, void* workspace,
+                              hipStream_t stream) {
+  const int nqb = (T + FA_QB - 1) / FA_QB, ntiles = (T + FA_KT - 1) / FA_KT;
   const long long items = (long long)nqb * bh, per = (items + 7) / 8;
   if (8 * per > 0x7fffffffLL) return -1;
-  const dim3 grid((unsigned)(8 * per)), block(64 * FA_WAVES);
   const uint16_t* qq = static_cast<const uint16_t*>(q);
   const uint16_t* kk = static_cast<const uint16_t*>(k);
   const uint16_t* vv = static_cast<const uint16_t*>(v);
+  uint4* kp = static_cast<uint4*>(workspace);
+  uint4* vp = kp + (size_t)bh * ntiles * 256;
   uint16_t* oo = static_cast<uint16_t*>(out);
+  hipLaunchKernelGGL(fa_pack_kernel, dim3(ntiles, bh), dim3(256), 0, stream, kk, vv, kp, vp, T,
+                     ntiles);
+  const dim3 grid((unsigned)(8 * per)), block(64 * FA_WAVES);
   if (f16)
-    hipLaunchKernelGGL(fa_bhwd_kernel<true>, grid, block, 0, stream, qq, kk, vv, oo, T, scale_log2,
+    hipLaunchKernelGGL(fa_bhwd_kernel<true>, grid, block, 0, stream, qq, kp, vp, oo, T, scale_log2,
                        nqb, (int)items, (int)per);
   else
-    hipLaunchKernelGGL(fa_bhwd_kernel<false>, grid, block, 0, stream, qq, kk, vv, oo, T, scale_log2,
-                       nqb, (int)items, (int)per);
+    hipLaunchKernelGGL(fa_bhwd_kernel<false>, grid, block, 0, stream, qq, kp, vp, oo, T,
+                       scale_log2, nqb, (int)items, (int)per);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

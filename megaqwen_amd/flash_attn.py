@@ -65,9 +65,15 @@ def flash_attn_bhwd(
         return out
     lib = _lib.load()
     dtype = _lib.MQ_DTYPE_F16 if q.dtype == torch.float16 else _lib.MQ_DTYPE_BF16
+    ws_bytes = lib.mq_flash_attn_workspace_bytes(b, h, t, d)
+    if ws_bytes == 0:
+        _lib.check(_lib.MQ_ERR_INVALID_ARG)
+    # K and V^T in MFMA-operand order, written and consumed within the call (stream-ordered, so
+    # the caching allocator may hand the block out again once the call is queued)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         _lib.check(lib.mq_flash_attn_bhwd(q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                           out.data_ptr(), b, h, t, d, dtype, float(scale),
-                                          stream))
+                                          ws.data_ptr(), ws_bytes, stream))
     return out

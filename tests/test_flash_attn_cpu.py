@@ -84,16 +84,28 @@ def test_c_abi_rejections():
     lib = _lib.load()
     fake = 1 << 20
     f = lib.mq_flash_attn_bhwd
-    assert f(fake, fake, fake, fake, 1, 1, 4, 128, _lib.MQ_DTYPE_BF16, 1.0, None) == _lib.MQ_ERR_INVALID_ARG
+    ws = lib.mq_flash_attn_workspace_bytes(1, 14, 1500, 64)
+    assert ws == 2 * 14 * 47 * 32 * 64 * 2                  # K and V^T copies, 32-key tiles
+    assert lib.mq_flash_attn_workspace_bytes(1, 1, 4, 128) == 0
+    W = 1 << 24
+    bf = _lib.MQ_DTYPE_BF16
+    assert f(fake, fake, fake, fake, 1, 1, 4, 128, bf, 1.0, W, 1 << 20, None) == _lib.MQ_ERR_INVALID_ARG
     assert b"head_dim=64" in lib.mq_last_error()
-    assert f(fake, fake, fake, fake, 1, 1, 4, 64, 7, 1.0, None) == _lib.MQ_ERR_INVALID_ARG
-    assert f(None, fake, fake, fake, 1, 1, 4, 64, _lib.MQ_DTYPE_BF16, 1.0, None) == _lib.MQ_ERR_INVALID_ARG
-    assert f(fake, fake, fake, fake, -1, 1, 4, 64, _lib.MQ_DTYPE_BF16, 1.0, None) == _lib.MQ_ERR_INVALID_ARG
-    assert f(fake, fake, fake, fake, 300, 300, 4, 64, _lib.MQ_DTYPE_F16, 1.0, None) == _lib.MQ_ERR_INVALID_ARG
+    assert f(fake, fake, fake, fake, 1, 1, 4, 64, 7, 1.0, W, 1 << 20, None) == _lib.MQ_ERR_INVALID_ARG
+    assert f(None, fake, fake, fake, 1, 1, 4, 64, bf, 1.0, W, 1 << 20, None) == _lib.MQ_ERR_INVALID_ARG
+    assert f(fake, fake, fake, fake, -1, 1, 4, 64, bf, 1.0, W, 1 << 20, None) == _lib.MQ_ERR_INVALID_ARG
+    assert f(fake, fake, fake, fake, 300, 300, 4, 64, _lib.MQ_DTYPE_F16, 1.0, W, 1 << 20, None) \
+        == _lib.MQ_ERR_INVALID_ARG
     assert b"65535" in lib.mq_last_error()
     # out overlapping v
-    assert f(fake, 2 * fake, 3 * fake, 3 * fake + 64, 1, 1, 4, 64, _lib.MQ_DTYPE_BF16, 1.0, None) \
+    assert f(fake, 2 * fake, 3 * fake, 3 * fake + 64, 1, 1, 4, 64, bf, 1.0, W, 1 << 20, None) \
         == _lib.MQ_ERR_INVALID_ARG
     assert b"overlap" in lib.mq_last_error()
+    # workspace too small, or missing
+    assert f(fake, 2 * fake, 3 * fake, 4 * fake, 1, 1, 40, 64, bf, 1.0, W, 100, None) \
+        == _lib.MQ_ERR_INVALID_ARG
+    assert b"workspace" in lib.mq_last_error()
+    assert f(fake, 2 * fake, 3 * fake, 4 * fake, 1, 1, 40, 64, bf, 1.0, None, 1 << 20, None) \
+        == _lib.MQ_ERR_INVALID_ARG
     # empty problems are no-ops (nothing is launched)
-    assert f(None, None, None, None, 1, 14, 0, 64, _lib.MQ_DTYPE_BF16, 1.0, None) == _lib.MQ_OK
+    assert f(None, None, None, None, 1, 14, 0, 64, bf, 1.0, None, 0, None) == _lib.MQ_OK
