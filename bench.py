@@ -467,14 +467,18 @@ def main():
 
     pf_best, pf_mean = time_prefill(dec, 512, 5)
     pf4_best, _ = time_prefill(dec, 4096, 2)
+    pf16_best, _ = time_prefill(dec, 16, 5)
+    pf64_best, _ = time_prefill(dec, 64, 5)
     prefill = {"tokens": 512, "ms": round(pf_mean * 1e3, 3), "tok_s": round(512 / pf_mean, 1),
                "mfma_util": round(prefill_flops(512) / pf_mean / MFMA_BF16_PEAK, 4),
                "tflops": round(prefill_flops(512) / pf_mean / 1e12, 1),
                "ms_4096": round(pf4_best * 1e3, 2),
-               "mfma_util_4096": round(prefill_flops(4096) / pf4_best / MFMA_BF16_PEAK, 4)}
+               "mfma_util_4096": round(prefill_flops(4096) / pf4_best / MFMA_BF16_PEAK, 4),
+               "ms_16": round(pf16_best * 1e3, 3), "ms_64": round(pf64_best * 1e3, 3)}
     print(f"[bench] prefill 512: {prefill['ms']} ms, {prefill['tok_s']} tok/s, "
           f"{prefill['tflops']} TFLOP/s = {prefill['mfma_util'] * 100:.1f}% of dense bf16 peak; "
-          f"4096: {prefill['ms_4096']} ms ({prefill['mfma_util_4096'] * 100:.1f}%)",
+          f"4096: {prefill['ms_4096']} ms ({prefill['mfma_util_4096'] * 100:.1f}%); 16: "
+          f"{prefill['ms_16']} ms; 64: {prefill['ms_64']} ms",
           file=sys.stderr, flush=True)
     head = res[128]
     achieved = head["bytes_per_token"] * head["tokens_per_launch"] / (head["launch_us"] * 1e-6)

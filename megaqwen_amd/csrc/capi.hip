@@ -220,6 +220,7 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   dec->ws = ws;
   mq_prefill_bind(&dec->pf, ws + lay.prefill, desc->max_prefill_len);
   if (mq_launch_clear_state(p.st, p.x, nullptr) != 0 ||
+      (dec->pf.cnt != nullptr && mq_launch_zero(dec->pf.cnt, dec->pf.cnt_bytes, nullptr) != 0) ||
       hipStreamSynchronize(nullptr) != hipSuccess) {
     delete dec;
     return fail(MQ_ERR_HIP, "state initialisation failed");
@@ -238,7 +239,8 @@ int mq_decoder_reset(mq_decoder* dec, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (mq_launch_zero(dec->p.kc, dec->kv_bytes, s) != 0 ||
       mq_launch_zero(dec->p.vc, dec->kv_bytes, s) != 0 ||
-      mq_launch_clear_state(dec->p.st, dec->p.x, s) != 0)
+      mq_launch_clear_state(dec->p.st, dec->p.x, s) != 0 ||
+      (dec->pf.cnt != nullptr && mq_launch_zero(dec->pf.cnt, dec->pf.cnt_bytes, s) != 0))
     return fail(MQ_ERR_HIP, "reset kernels failed to launch");
   dec->pos = 0;
   return MQ_OK;

@@ -13,6 +13,10 @@ struct MqPrefillBuffers {
   bf16_t* vt;    // V^T of each kv head in attention-operand tile order (prefill.hip vt_index)
   bf16_t* kt;    // K of each kv head in attention-operand tile order (prefill.hip kt_index)
   int ntiles;    // 32-key tiles per kv head in vt / kt (max_n rounded up)
+  float* part;   // split-K fp32 partials of the GEMMs (prefill.hip gemm_plan)
+  uint32_t* cnt; // split-K arrival counters, one per output tile; zero between GEMMs (cleared
+                 // with the decoder state, reset by the last split of each tile)
+  size_t cnt_bytes;
 };
 
 size_t mq_prefill_workspace_bytes(int max_n);

@@ -138,6 +138,13 @@ struct GemmArgs {
   bf16_t* Kt;
   int max_seq;
   int M, N, K;
+  // split-K (gridDim.z = sk > 1): every split writes its fp32 partial tile to `part` with
+  // device-coherent stores; the last split of a tile to arrive (counter `cnt[tile]`, reset by
+  // it to 0) sums the sk partials in split order and runs the epilogue, so the result does not
+  // depend on which split finishes last
+  int sk;
+  float* part;       // [tiles][sk][elements per thread][threads]
+  uint32_t* cnt;     // [tiles], 0 between uses
 };
 
 #define GEMM_BK 64           // K per step of 64- and 128-row tiles (32-row tiles: 128)
@@ -254,6 +261,7 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
   const int wm = KG == 1 ? (wave >> 1) : 0;
   const int wk = KG == 2 ? (wave >> 1) : 0;
   const int n_base = blockIdx.x * BN, m_base = blockIdx.y * BM;
+  const int kslice = g.K / g.sk, k_first = (int)blockIdx.z * kslice;   // this split's K range
   const bf16_t* B;
   if (n_base < g.n0) B = g.B0 + (size_t)n_base * g.K;
   else if (n_base < g.n1) B = g.B1 + (size_t)(n_base - g.n0) * g.K;
@@ -267,11 +275,11 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
     const int am = min(m_base + sr + RPP * i, g.M - 1);
-    a_src[i] = g.A + (size_t)am * g.lda + sk;
+    a_src[i] = g.A + (size_t)am * g.lda + k_first + sk;
   }
   const bf16_t* b_src[NB];
-  b_src[0] = B + (size_t)sr * g.K + sk;
-  if (NB == 2) b_src[NB - 1] = Bu + (size_t)sr * g.K + sk;
+  b_src[0] = B + (size_t)sr * g.K + k_first + sk;
+  if (NB == 2) b_src[NB - 1] = Bu + (size_t)sr * g.K + k_first + sk;
 
   uint4 ra[S][NA], rb[S][NB][NL];
   auto load_step = [&](int k, uint4 (&a)[NA], uint4 (&b)[NB][NL]) {
@@ -353,9 +361,8 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
   // Schedule (all slot and buffer indices compile-time, so each step is straight-line code and
   // the loads of a slot are waited for only when that slot is stored): step k stores slot
   // (k + 1) % S into LDS buffer (k + 1) % 2, refills slot k % S with step k + S and multiplies
-  // buffer k % 2.  K / BK is a multiple of S (every K of the model is a multiple of 512, see the
-  // static_assert at the launcher).
-  const int nk = g.K / BK;
+  // buffer k % 2.  The split's K / BK is a multiple of S (the launcher picks sk so).
+  const int nk = kslice / BK;
 #pragma unroll
   for (int s = 0; s < S; ++s) load_step(s, ra[s], rb[s]);
   store_step(0, ra[0], rb[0]);
@@ -387,6 +394,57 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
     if (wk == 1) return;
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[0][0][0][j] += red[(wn * 16 + j) * 64 + lane];
+  }
+
+  if (g.sk > 1) {
+    // split-K fixup (the waves left after the K-group merge: 128 or 256 threads)
+    constexpr int E = NB * MB * NBK * 16;
+    constexpr int NT = KG == 2 ? 128 : 256;
+    __shared__ uint32_t is_last;
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    float* mine = g.part + ((size_t)tile * g.sk + blockIdx.z) * E * NT + t;
+    {
+      int e = 0;
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j, ++e) st_coh(mine + (size_t)e * NT, acc[b][mb][nb][j]);
+    }
+    wait_all_memory();            // this thread's partial is stored ...
+    __syncthreads();              // ... and every other thread's
+    if (t == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(g.cnt + tile, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      is_last = prev + 1 == (uint32_t)g.sk;
+      if (is_last) __hip_atomic_store(g.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    const float* base = g.part + (size_t)tile * g.sk * E * NT + t;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) acc[b][mb][nb][j] = 0.f;
+    for (int sp = 0; sp < g.sk; ++sp) {
+      const float* src = base + (size_t)sp * E * NT;
+      int e = 0;
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j, ++e) acc[b][mb][nb][j] += ld_coh(src + (size_t)e * NT);
+    }
   }
 
   if constexpr (EPI == EPI_QKV) {
@@ -677,11 +735,16 @@ static size_t pf_align(size_t v) { return (v + 255) / 256 * 256; }
 // 32-key tiles per kv head of the K / V^T operand copies
 static int pf_tiles(int max_n) { return (max_n + 31) / 32; }
 
+static void pf_split_sizes(int max_n, size_t& part_bytes, size_t& tiles);
+
 size_t mq_prefill_workspace_bytes(int max_n) {
   if (max_n <= 0) return 0;
   const size_t n = (size_t)max_n;
+  size_t part, tiles;
+  pf_split_sizes(max_n, part, tiles);
   return pf_align(n * MQ_H * 2) * 2 + pf_align(n * MQ_QKV * 2) + pf_align(n * MQ_QDIM * 2) +
-         pf_align(n * MQ_I * 2) + 2 * pf_align((size_t)MQ_NKV * pf_tiles(max_n) * 4096 * 2);
+         pf_align(n * MQ_I * 2) + 2 * pf_align((size_t)MQ_NKV * pf_tiles(max_n) * 4096 * 2) +
+         pf_align(part) + pf_align(tiles * 4);
 }
 
 void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n) {
@@ -690,6 +753,9 @@ void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n) {
     b->h = b->xn = b->qkv = b->att = b->m = b->vt = nullptr;
     b->kt = nullptr;
     b->ntiles = 0;
+    b->part = nullptr;
+    b->cnt = nullptr;
+    b->cnt_bytes = 0;
     return;
   }
   const size_t n = (size_t)max_n;
@@ -703,6 +769,13 @@ void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n) {
   b->ntiles = pf_tiles(max_n);
   c += pf_align((size_t)MQ_NKV * b->ntiles * 4096 * 2);
   b->kt = reinterpret_cast<bf16_t*>(c);
+  c += pf_align((size_t)MQ_NKV * b->ntiles * 4096 * 2);
+  size_t part, tiles;
+  pf_split_sizes(max_n, part, tiles);
+  b->part = reinterpret_cast<float*>(c);
+  c += pf_align(part);
+  b->cnt = reinterpret_cast<uint32_t*>(c);
+  b->cnt_bytes = pf_align(tiles * 4);
 }
 
 // K must be a multiple of 512 and N of 128 (every Qwen3-0.6B projection is).
@@ -711,33 +784,89 @@ static_assert(MQ_H % 512 == 0 && MQ_QDIM % 512 == 0 && MQ_I % 512 == 0, "GEMM K 
 // 128 x 128 (128 x 64 for the two SwiGLU matrices) when that still gives >= 512 workgroups
 // (two per CU; large M); otherwise 64 x 64, or 32 x 64 when even 64-row tiles would leave CUs
 // idle (the N = 1024 GEMMs at M <= 1024).
+//
+// Tile and split plan of one GEMM (shared by the launcher and the workspace sizing).
+struct GemmPlan {
+  int bm, bn, gx, gy, sk, nb;
+};
+// Smallest split of K that gives >= 480 workgroups (about two per CU), else the largest
+// allowed: a split's K must hold a whole ring of steps (BK x S).
+static int pick_sk(int tiles, int K, int bk, int stages) {
+  const int cands[] = {1, 2, 3, 4, 6, 8};
+  int best = 1;
+  for (int sk : cands) {
+    if (K % sk != 0 || (K / sk) % (bk * stages) != 0) continue;
+    best = sk;
+    if (tiles * sk >= 480) break;
+  }
+  return best;
+}
 template <int EPI>
-static void gemm(const GemmArgs& g, hipStream_t s) {
-  const int mt128 = (g.M + 127) / 128;
+static GemmPlan gemm_plan(int M, int N, int K) {
+  const int mt128 = (M + 127) / 128;
+  GemmPlan pl{64, 64, N / 64, (M + 63) / 64, 1, EPI == EPI_SWIGLU ? 2 : 1};
   if constexpr (EPI == EPI_SWIGLU) {
-    if ((g.N / 64) * mt128 >= 512) {
-      pf_gemm_kernel<EPI, 128, 64><<<dim3(g.N / 64, mt128), 256, 0, s>>>(g);
-      return;
-    }
+    if ((N / 64) * mt128 >= 512) pl = GemmPlan{128, 64, N / 64, mt128, 1, 2};
   } else if constexpr (EPI == EPI_QKV) {
     // one 128-column head per tile
-    if ((g.N / 128) * mt128 >= 512)
-      pf_gemm_kernel<EPI, 128, 128><<<dim3(g.N / 128, mt128), 256, 0, s>>>(g);
-    else
-      pf_gemm_kernel<EPI, 64, 128><<<dim3(g.N / 128, (g.M + 63) / 64), 256, 0, s>>>(g);
-    return;
+    if ((N / 128) * mt128 >= 512) pl = GemmPlan{128, 128, N / 128, mt128, 1, 1};
+    else pl = GemmPlan{64, 128, N / 128, (M + 63) / 64, 1, 1};
   } else {
-    if ((g.N / 128) * mt128 >= 512) {
-      pf_gemm_kernel<EPI, 128, 128><<<dim3(g.N / 128, mt128), 256, 0, s>>>(g);
-      return;
-    }
-    if ((g.N / 64) * ((g.M + 63) / 64) < 256) {
-      pf_gemm_kernel<EPI, 32, 64><<<dim3(g.N / 64, (g.M + 31) / 32), 256, 0, s>>>(g);
-      return;
-    }
+    if ((N / 128) * mt128 >= 512) pl = GemmPlan{128, 128, N / 128, mt128, 1, 1};
+    else if ((N / 64) * ((M + 63) / 64) < 256) pl = GemmPlan{32, 64, N / 64, (M + 31) / 32, 1, 1};
   }
-  if constexpr (EPI != EPI_QKV)
-    pf_gemm_kernel<EPI, 64, 64><<<dim3(g.N / 64, (g.M + 63) / 64), 256, 0, s>>>(g);
+  // K is split only for the 32 x 64 tiles of short prompts (fewer than 128 tiles, so at most
+  // half the CUs busy): there a split's partial is 8 KB and the fixup costs less than the
+  // longer K loop it removes (O and down at 16 tokens: 11.8 -> 9.5-10 us).  Larger tiles pay
+  // more for the partial round trip than they save (q|k|v and gate|up at 16 tokens 12-12.4 ->
+  // 12.9-13.5 us with 4 splits; every GEMM at 512 tokens slower with 2 splits, e.g. gate|up
+  // 18.0 -> 23.9 us).
+  if (pl.bm == 32 && pl.gx * pl.gy < 128) pl.sk = pick_sk(pl.gx * pl.gy, K, 128, GEMM_STAGES);
+  return pl;
+}
+// fp32 partial bytes of a plan (0 without a split)
+static size_t plan_part_bytes(const GemmPlan& pl) {
+  return pl.sk > 1 ? (size_t)pl.gx * pl.gy * pl.sk * pl.bm * pl.bn * pl.nb * 4 : 0;
+}
+
+template <int EPI>
+static void gemm(GemmArgs g, const MqPrefillBuffers& b, hipStream_t s) {
+  const GemmPlan pl = gemm_plan<EPI>(g.M, g.N, g.K);
+  g.sk = pl.sk;
+  g.part = b.part;
+  g.cnt = b.cnt;
+  const dim3 grid(pl.gx, pl.gy, pl.sk);
+  if (pl.bm == 128 && pl.bn == 64) {
+    if constexpr (EPI == EPI_SWIGLU) pf_gemm_kernel<EPI, 128, 64><<<grid, 256, 0, s>>>(g);
+  } else if (pl.bm == 128) {
+    if constexpr (EPI != EPI_SWIGLU) pf_gemm_kernel<EPI, 128, 128><<<grid, 256, 0, s>>>(g);
+  } else if (pl.bm == 64 && pl.bn == 128) {
+    if constexpr (EPI == EPI_QKV) pf_gemm_kernel<EPI, 64, 128><<<grid, 256, 0, s>>>(g);
+  } else if (pl.bm == 32) {
+    if constexpr (EPI != EPI_QKV && EPI != EPI_SWIGLU)
+      pf_gemm_kernel<EPI, 32, 64><<<grid, 256, 0, s>>>(g);
+  } else {
+    if constexpr (EPI != EPI_QKV) pf_gemm_kernel<EPI, 64, 64><<<grid, 256, 0, s>>>(g);
+  }
+}
+
+// Largest split-K partial area and tile count over every prompt length up to max_n.
+static void pf_split_sizes(int max_n, size_t& part_bytes, size_t& tiles) {
+  part_bytes = 0;
+  tiles = 0;
+  for (int m = 1; m <= max_n; m = (m < 32 ? 32 : m + 32)) {
+    const int mm = m > max_n ? max_n : m;
+    const GemmPlan ps[] = {gemm_plan<EPI_QKV>(mm, MQ_QKV, MQ_H),
+                           gemm_plan<EPI_RESID>(mm, MQ_H, MQ_QDIM),
+                           gemm_plan<EPI_SWIGLU>(mm, MQ_I, MQ_H),
+                           gemm_plan<EPI_RESID>(mm, MQ_H, MQ_I)};
+    for (const GemmPlan& pl : ps) {
+      part_bytes = part_bytes > plan_part_bytes(pl) ? part_bytes : plan_part_bytes(pl);
+      const size_t t = (size_t)pl.gx * pl.gy;
+      tiles = tiles > t ? tiles : t;
+    }
+    if (mm == max_n) break;
+  }
 }
 
 int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefillBuffers& b,
@@ -762,25 +891,25 @@ int mq_launch_prefill(const MqDecodeParams& p, const MqLayerW* hl, const MqPrefi
     g.kcl = p.kc + (size_t)l * MQ_NKV * p.max_seq * MQ_D;
     g.vcl = p.vc + (size_t)l * MQ_NKV * p.max_seq * MQ_D;
     g.Kt = b.kt;
-    gemm<EPI_QKV>(g, stream);
+    gemm<EPI_QKV>(g, b, stream);
     pf_attn_kernel<<<dim3(MQ_NQ, (n + 31) / 32), 64 * ATT_SPLIT, 0, stream>>>(
         p, l, b.qkv, b.kt, b.vt, b.ntiles, b.att, n);
     g = GemmArgs{};
     g.A = b.att; g.lda = MQ_QDIM;
     g.B0 = g.B1 = g.B2 = w.wo; g.n0 = g.n1 = MQ_H;
     g.C = b.h; g.ldc = MQ_H; g.R = b.h; g.ldr = MQ_H; g.M = n; g.N = MQ_H; g.K = MQ_QDIM;
-    gemm<EPI_RESID>(g, stream);
+    gemm<EPI_RESID>(g, b, stream);
     pf_rmsnorm_kernel<<<n, 128, 0, stream>>>(b.h, w.post_ln, b.xn);
     g = GemmArgs{};
     g.A = b.xn; g.lda = MQ_H;
     g.B0 = g.B1 = g.B2 = w.wg; g.n0 = g.n1 = MQ_I; g.Bu = w.wu;
     g.C = b.m; g.ldc = MQ_I; g.M = n; g.N = MQ_I; g.K = MQ_H;
-    gemm<EPI_SWIGLU>(g, stream);
+    gemm<EPI_SWIGLU>(g, b, stream);
     g = GemmArgs{};
     g.A = b.m; g.lda = MQ_I;
     g.B0 = g.B1 = g.B2 = w.wd; g.n0 = g.n1 = MQ_H;
     g.C = b.h; g.ldc = MQ_H; g.R = b.h; g.ldr = MQ_H; g.M = n; g.N = MQ_H; g.K = MQ_I;
-    gemm<EPI_RESID>(g, stream);
+    gemm<EPI_RESID>(g, b, stream);
     if (trace != nullptr &&
         hipMemcpyAsync(trace + (size_t)l * n * MQ_H, b.h, (size_t)n * MQ_H * sizeof(bf16_t),
                        hipMemcpyDeviceToDevice, stream) != hipSuccess)
