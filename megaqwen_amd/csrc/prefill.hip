@@ -14,8 +14,8 @@
 // then the last row's final norm (bf16) and the LM-head argmax (fused_prefill_kernels.inl:655-824).
 //
 // GEMMs are C[M,N] = A[M,K] B[N,K]^T ("NT": activations and weights both K-contiguous) on
-// v_mfma_f32_32x32x16_bf16 with fp32 accumulation: 128x128, 64x64 or 32x64 workgroup tiles (by
-// M), K staged through double-buffered LDS in steps of 64 (128 for 32-row tiles), fed by a
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulation: 128x128, 128x64, 64x64 or 32x64 workgroup
+// tiles (by M and N), K staged through double-buffered LDS in steps of 64 (128 for 32-row tiles), fed by a
 // register ring of global loads.  Consecutive workgroups walk N first, so with N/BN a multiple
 // of 8 all M tiles of one weight tile land on one XCD and share its L2.
 #include "mq_prefill.h"
@@ -150,7 +150,10 @@ struct GemmArgs {
 #define GEMM_BK 64           // K per step of 64- and 128-row tiles (32-row tiles: 128)
 #define GEMM_STAGES 4        // K steps whose global loads are in flight in registers (64-row and
                              // 32-row tiles)
-#define GEMM_STAGES_BIG 2    // the same for 128-row tiles, so two of their waves fit on a SIMD
+#define GEMM_STAGES_BIG 4    // the same for 128-row tiles (172-177 VGPRs: still two waves per
+                             // SIMD); 2 stages measured ~1% slower per 4096-token prefill
+static_assert(512 / GEMM_BK % GEMM_STAGES == 0 && 512 / GEMM_BK % GEMM_STAGES_BIG == 0,
+              "every K (a multiple of 512) is a whole number of register-ring rounds");
 
 // One BM x BN tile of C per workgroup of 4 waves, K in steps of 64.  The global loads of step
 // k + S are issued while step k is multiplied: a ring of S register slots (GEMM_STAGES, or
@@ -782,8 +785,10 @@ void mq_prefill_bind(MqPrefillBuffers* b, char* base, int max_n) {
 static_assert(MQ_H % 512 == 0 && MQ_QDIM % 512 == 0 && MQ_I % 512 == 0, "GEMM K steps");
 // Tile choice:
 // 128 x 128 (128 x 64 for the two SwiGLU matrices) when that still gives >= 512 workgroups
-// (two per CU; large M); otherwise 64 x 64, or 32 x 64 when even 64-row tiles would leave CUs
-// idle (the N = 1024 GEMMs at M <= 1024).
+// (two per CU; large M); for the N = 1024 GEMMs (O, down) 128 x 64 when that gives >= 512
+// (M >= 4096: the 64 x 64 tiles' waves wait on LDS issue, three LDS instructions per MFMA;
+// 4096-token prefill 9.6 -> 9.4 ms with the 4-stage ring above); otherwise 64 x 64, or 32 x 64
+// when even 64-row tiles would leave CUs idle (M <= 1024).
 //
 // Tile and split plan of one GEMM (shared by the launcher and the workspace sizing).
 struct GemmPlan {
@@ -813,6 +818,7 @@ static GemmPlan gemm_plan(int M, int N, int K) {
     else pl = GemmPlan{64, 128, N / 128, (M + 63) / 64, 1, 1};
   } else {
     if ((N / 128) * mt128 >= 512) pl = GemmPlan{128, 128, N / 128, mt128, 1, 1};
+    else if ((N / 64) * mt128 >= 512) pl = GemmPlan{128, 64, N / 64, mt128, 1, 1};
     else if ((N / 64) * ((M + 63) / 64) < 256) pl = GemmPlan{32, 64, N / 64, (M + 31) / 32, 1, 1};
   }
   // K is split only for the 32 x 64 tiles of short prompts (fewer than 128 tiles, so at most
@@ -837,7 +843,7 @@ static void gemm(GemmArgs g, const MqPrefillBuffers& b, hipStream_t s) {
   g.cnt = b.cnt;
   const dim3 grid(pl.gx, pl.gy, pl.sk);
   if (pl.bm == 128 && pl.bn == 64) {
-    if constexpr (EPI == EPI_SWIGLU) pf_gemm_kernel<EPI, 128, 64><<<grid, 256, 0, s>>>(g);
+    if constexpr (EPI != EPI_QKV) pf_gemm_kernel<EPI, 128, 64><<<grid, 256, 0, s>>>(g);
   } else if (pl.bm == 128) {
     if constexpr (EPI != EPI_SWIGLU) pf_gemm_kernel<EPI, 128, 128><<<grid, 256, 0, s>>>(g);
   } else if (pl.bm == 64 && pl.bn == 128) {
