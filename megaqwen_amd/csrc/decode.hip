@@ -254,10 +254,13 @@ MQ_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 MQ_DEV void norm_1024(const float* x, const bf16_t* __restrict__ w, float* xn, float* red,
                       bool round_out = false) {
   const int t = tid();
+  // the weights are loaded before the reduction: a load after block_sum's barriers cannot be
+  // hoisted above them and put its latency on every norm's critical path (572 against 576 us per
+  // token at pos 128)
+  const uint32_t wv = ld32(w + 2 * t);
   const float2 v = reinterpret_cast<const float2*>(x)[t];
   const float ss = block_sum(v.x * v.x + v.y * v.y, red);
   const float r = rsqrtf(ss * (1.0f / MQ_H) + MQ_EPS);
-  const uint32_t wv = ld32(w + 2 * t);
   float y0 = v.x * r * bf16_lo(wv), y1 = v.y * r * bf16_hi(wv);
   if (round_out) {
     y0 = round_bf16(y0);
