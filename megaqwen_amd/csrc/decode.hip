@@ -9,16 +9,19 @@
 //   P4  RMSNorm(a) + gate/up GEMVs (2 x 3072 x 1024) + silu(g) * u
 //   P5  down GEMV (1024 x 3072) + residual, rounded to bf16 (the layer output)
 //   LM  final RMSNorm + LM-head GEMV (vocab x 1024) + argmax (packed 64-bit atomic max)
-// The phases run either inside one persistent cooperative kernel separated by grid barriers
-// (5 per layer = 140 per token, against 225 in the reference's ldg_decode_kernel,
+// The phases run either inside one persistent cooperative kernel, which hands data between
+// workgroups through device-coherent exchange words that carry the layer's epoch (no grid
+// barrier at all; one kv-head-group barrier per layer above 176 cache positions, against 225
+// grid.sync() per token in the reference's ldg_decode_kernel,
 // csrc/megakernel/fused_decode_ldg_kernel.inl:5-259), or as one kernel launch per phase.
 //
 // Workgroup organisation (512 threads): waves 0..6 are compute waves, wave 7 is the sync wave.
-// Per phase the compute waves finish their dot products, publish outputs with coherent (sc1)
-// stores, wait for them, then issue the NEXT phase's weight loads into registers; the sync wave
-// meanwhile runs the grid barrier and, once it opens, loads the next phase's input vector into
-// LDS.  Because gfx9 returns a wave's loads in order, keeping the prefetches out of the sync
-// wave is what lets the barrier and the input broadcast proceed while weights stream in.
+// Per phase the compute waves finish their dot products; the sync wave publishes the outputs with
+// coherent (sc1) stores; then the compute waves issue the NEXT phase's weight loads into
+// registers while the sync wave (or, for the two larger exchanges, every wave) polls the next
+// phase's input words until they carry the expected epoch and copies them into LDS.  Because gfx9
+// returns a wave's loads in order, keeping the prefetches out of the sync wave is what lets the
+// exchange proceed while weights stream in.
 // Residuals stay in registers: a workgroup owns the same hidden rows in the O and down phases.
 //
 // Numerics follow the reference decode path: fp32 activations and accumulation, bf16 weights,
@@ -216,18 +219,18 @@ MQ_DEV void x_gather(float* dst, float* dst2, const uint64_t* src, uint32_t e, M
   });
 }
 
-// Phase boundary.  Compute waves arrive with this phase's dot products in LDS and the next
-// phase's weight prefetch in flight.  The sync wave then runs `epilogue()` (finishes this
-// phase's outputs and publishes them with coherent stores), waits for those stores, runs the
-// grid barrier (when `barrier`) and `input()` (the next phase's input vector into LDS).  The
-// compute waves never wait for a store, so their prefetches are never waited on either.
+// Phase boundary inside one kernel of the one-kernel-per-phase mode and the op-level kernels
+// (the kernel boundaries order the phases).  Compute waves arrive with this phase's dot products
+// in LDS and the next phase's weight prefetch in flight.  The sync wave then runs `epilogue()`
+// (finishes this phase's outputs and publishes them with coherent stores), waits for those
+// stores and runs `input()` (the next phase's input vector into LDS).  The compute waves never
+// wait for a store, so their prefetches are never waited on either.
 template <class Epi, class Input>
-MQ_DEV void phase_sync(MqSync* sy, uint32_t target, bool barrier, Epi epilogue, Input input) {
+MQ_DEV void phase_sync(Epi epilogue, Input input) {
   __syncthreads();
   if (wave_id() == MQ_SYNC_WAVE) {
     epilogue();
     wait_all_memory();
-    if (barrier) grid_barrier_wave(sy, target);
     input();
     wait_all_memory();
   }
@@ -240,6 +243,60 @@ MQ_DEV void phase_finish(Epi epilogue) {
   if (wave_id() == MQ_SYNC_WAVE) epilogue();
 }
 #define MQ_NOTHING [] {}
+// Tagged fp32 exchange words (the O-projection partials and the MLP vector): the two lowest
+// mantissa bits of each value carry the low two bits of the layer's exchange epoch, so a reader
+// polls the data itself, with no store acknowledgement, counter or separate barrier.  The buffers
+// alternate by layer parity, so the word a reader may see before the new one was written two
+// layers back (or one, across a step boundary when the layer count is odd): its epoch differs
+// by 1..2, and so do the two tag bits.  A workgroup cannot run two layers ahead of another, since
+// every layer needs every workgroup's values.  Every mode publishes and reads the same
+// truncated values (the one-kernel-per-phase mode with tag 0 and no polling), so the modes stay
+// bit-identical; the truncation is below 2^-22 relative, far under the bf16 rounding these
+// values meet downstream.
+MQ_DEV uint32_t tag_bits(float v, uint32_t e) { return (__float_as_uint(v) & ~3u) | (e & 3u); }
+MQ_DEV float untag(uint32_t u) { return __uint_as_float(u & ~3u); }
+MQ_DEV void st_tag(float* p, float v, uint32_t e) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), tag_bits(v, e), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+MQ_DEV bool tag_ok2(uint64_t w, uint32_t tag) {
+  return ((uint32_t)w & 3u) == tag && ((uint32_t)(w >> 32) & 3u) == tag;
+}
+// All threads: P 64-bit words per thread (two tagged values each, word idx(i)) polled until both
+// tags are `tag` (tag < 0: taken as they are), then out(i, lo, hi) with the tags removed.  Only
+// stale words are loaded again.  A set error flag (read on every 16th round) or the spin bound
+// ends the wait early, as in x_poll.
+template <int P, class Idx, class Out>
+MQ_DEV void tag_poll_all(const float* src, Idx idx, int tag, MqSync* sy, Out out) {
+  uint64_t w[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) w[i] = ld_coh64(reinterpret_cast<const uint64_t*>(src) + idx(i));
+  if (tag >= 0) {
+    uint32_t spins = 0;
+    while (true) {
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < P; ++i) ok = ok && tag_ok2(w[i], (uint32_t)tag);
+      if (__all(ok)) break;
+      uint32_t ev = 0;
+      if (lane_id() == 0 && (spins & 15) == 15)
+        ev = __hip_atomic_load(&sy->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_amdgcn_readlane(ev, 0) != 0) break;
+      if (++spins > MQ_SPIN_LIMIT) {
+        if (lane_id() == 0)
+          __hip_atomic_store(&sy->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int i = 0; i < P; ++i)
+        if (!tag_ok2(w[i], (uint32_t)tag))
+          w[i] = ld_coh64(reinterpret_cast<const uint64_t*>(src) + idx(i));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < P; ++i) out(i, untag((uint32_t)w[i]), untag((uint32_t)(w[i] >> 32)));
+}
 
 // 2^x with the hardware v_exp_f32 (results below the normal range flush to zero, as the
 // reference's fast-math __expf does); used for softmax weights, whose arguments are <= 0.
@@ -808,15 +865,15 @@ MQ_DEV void gu_run(const GateUpSet& ws, const MqLayerW& w, int wg, int G, float*
 }
 // Sync-wave epilogue: m = silu(g) * u with silu(x) = x / (1 + e^-x)
 // (fused_decode_ldg_mlp.inl:120-175, fused_decode_ldg_common.inl:123-125), published to every
-// group's copy of m [MQ_GROUPS][MQ_I] (passed by a counter barrier).
-MQ_DEV void gu_publish(float* m, int wg, int G, const float* lds) {
+// group's copy of m [MQ_GROUPS][MQ_I] as tagged words of epoch e (tag_bits).
+MQ_DEV void gu_publish(float* m, int wg, int G, const float* lds, uint32_t e) {
   int r0, nr;
   row_range(MQ_I, wg, G, r0, nr);
   for (int t = lane_id(); t < nr; t += 64) {
     const float gv = lds[LDS_PR + t], uv = lds[LDS_PR + nr + t];
     const float v = gv / (1.0f + expf(-gv)) * uv;
 #pragma unroll
-    for (int c = 0; c < MQ_GROUPS; ++c) st_coh(m + (size_t)c * MQ_I + r0 + t, v);
+    for (int c = 0; c < MQ_GROUPS; ++c) st_tag(m + (size_t)c * MQ_I + r0 + t, v, e);
   }
 }
 // The op-level form (fp32 array, plain coherent stores).
@@ -927,10 +984,7 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
       old = __hip_atomic_fetch_add(&sy->done.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (__builtin_amdgcn_readlane(old, 0) == (uint32_t)G - 1) {
-      // the last workgroup: token, then the step's sync state cleared by the whole wave
-      for (int i = lane; i < MQ_BAR_COPIES * MQ_BAR_STRIPES; i += 64)
-        __hip_atomic_store(&sy->bar[i / MQ_BAR_STRIPES][i % MQ_BAR_STRIPES].v, 0u,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the last workgroup: token, then the step's sync state cleared
       if (lane < MQ_NKV)
         __hip_atomic_store(&sy->attn[lane].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (lane == 0) {
@@ -964,16 +1018,19 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
 // a group shares one XCD and its L2; every exchange still uses device-scope (sc1) operations, so
 // correctness does not depend on that placement, only the cost of the group-local steps does.
 // Per layer:
-//   1. q|k|v: group h computes the 512 rows of its kv head (q heads 2h, 2h+1, k and v of h).
-//   2. group barrier; attention split over the group's workgroups by position chunks, partials
-//      (m, l, o) published per chunk.
+//   1. q|k|v: group h computes the 512 rows of its kv head (q heads 2h, 2h+1, k and v of h),
+//      published as (value, epoch) words read by the group.
+//   2. attention split over the group's workgroups by position chunks, partials (m, l, o)
+//      published per chunk.
 //   3. group barrier; every workgroup of the group merges the partials (att of its two query
-//      heads) and computes its rows of the O projection restricted to the head's 256 columns.
-//   4. grid barrier; a = x + sum_h opart_h, RMSNorm, gate|up rows.
-//   5. grid barrier; down rows + a -> bf16 layer output.   6. grid barrier -> next layer.
-// That is 3 grid-wide and 2 group-local barriers per layer.  For short contexts (cache length
+//      heads) and computes its rows of the O projection restricted to the head's 256 columns,
+//      published as tagged words to every group's copy.
+//   4. a = x + sum_h opart_h (every thread polls its rows), RMSNorm, gate|up rows; silu(g) * u
+//      published as tagged words.
+//   5. down rows + a -> bf16 layer output, published as (bf16 pair, epoch) words -> next layer.
+// That is 4 exchanges and no grid-wide barrier per layer.  For short contexts (cache length
 // <= attn_local_max) steps 2-3 collapse: every workgroup of the group attends over all
-// positions itself (its O rows prefetched with the K/V rows), and the merge barrier goes away.
+// positions itself (its O rows prefetched with the K/V rows), and the group barrier goes away.
 // Measured per layer (MFMA scores, epoch-word exchanges): at 128 positions local mode takes
 // 18.7 us against 19.2 us split; at 200 positions 19.7 against 19.6, so the default switches
 // to split chunks above 176 positions.
@@ -1130,21 +1187,23 @@ MQ_DEV void opart_run(const OPairSet& ws, const MqLayerW& w, int h, int j, int N
   ws.compute([&](int i) { return opart_row(w, h, r0 + i); }, nr, lds + LDS_ATTH,
              [&](int i, float v) { lds[LDS_PR + i] = v; });
 }
-// opart: MqExchange.opart [MQ_GROUPS copies][MQ_NKV][MQ_H]; each value goes to every copy.
-MQ_DEV void opart_publish(float* opart, int h, int j, int NG, const float* lds) {
+// opart: one layer-parity half of MqExchange.opart, [MQ_GROUPS copies][MQ_NKV][MQ_H]; each
+// value goes to every copy as a tagged word of epoch e (tag_bits).
+MQ_DEV void opart_publish(float* opart, int h, int j, int NG, const float* lds, uint32_t e) {
   int r0, nr;
   row_range(MQ_H, j, NG, r0, nr);
   for (int t = lane_id(); t < nr; t += 64) {
     const float v = lds[LDS_PR + t];
 #pragma unroll
-    for (int c = 0; c < MQ_GROUPS; ++c) st_coh(opart + (c * MQ_NKV + h) * MQ_H + r0 + t, v);
+    for (int c = 0; c < MQ_GROUPS; ++c) st_tag(opart + (c * MQ_NKV + h) * MQ_H + r0 + t, v, e);
   }
 }
 // a = x + sum_h opart_h, summed in head order (the single-row form for the multi-kernel mode).
 MQ_DEV float a_elem(float x, const float* opart, int r) {
   float a = x;
 #pragma unroll
-  for (int h = 0; h < MQ_NKV; ++h) a += ld_coh(opart + h * MQ_H + r);
+  for (int h = 0; h < MQ_NKV; ++h)
+    a += untag(__float_as_uint(ld_coh(opart + h * MQ_H + r)));
   return a;
 }
 // Sync wave: a for all 1024 rows from the layer input in LDS_HID -> LDS_IN (gate|up input) and
@@ -1165,8 +1224,8 @@ MQ_DEV void gu_input(const float* opart, float* lds) {
       float2 a = reinterpret_cast<const float2*>(lds + LDS_HID)[q];
 #pragma unroll
       for (int h = 0; h < MQ_NKV; ++h) {
-        a.x += o[i][h].x;
-        a.y += o[i][h].y;
+        a.x += untag(__float_as_uint(o[i][h].x));
+        a.y += untag(__float_as_uint(o[i][h].y));
       }
       reinterpret_cast<float2*>(lds + LDS_IN)[q] = a;
       reinterpret_cast<float2*>(lds + LDS_A)[q] = a;
@@ -1175,21 +1234,31 @@ MQ_DEV void gu_input(const float* opart, float* lds) {
 }
 // All threads: a for all 1024 rows (thread t: rows 2t, 2t+1), same summation order as
 // gu_input and a_elem; ends with __syncthreads.
-MQ_DEV void gu_input_all(const float* opart, float* lds) {
+MQ_DEV void gu_input_all(const float* opart, float* lds, int tag, MqSync* sy) {
   const int t = tid();
-  if (t < MQ_H / 2) {
-    float2 o[MQ_NKV];
+  static_assert(MQ_H / 2 == MQ_THREADS, "one row pair per thread");
+  float2 o[MQ_NKV];
+  tag_poll_all<MQ_NKV>(opart, [&](int h) { return (h * MQ_H) / 2 + t; }, tag, sy,
+                       [&](int h, float lo, float hi) { o[h] = make_float2(lo, hi); });
+  float2 a = reinterpret_cast<const float2*>(lds + LDS_HID)[t];
 #pragma unroll
-    for (int h = 0; h < MQ_NKV; ++h) o[h] = ld_coh2(opart + h * MQ_H + 2 * t);
-    float2 a = reinterpret_cast<const float2*>(lds + LDS_HID)[t];
-#pragma unroll
-    for (int h = 0; h < MQ_NKV; ++h) {
-      a.x += o[h].x;
-      a.y += o[h].y;
-    }
-    reinterpret_cast<float2*>(lds + LDS_IN)[t] = a;
-    reinterpret_cast<float2*>(lds + LDS_A)[t] = a;
+  for (int h = 0; h < MQ_NKV; ++h) {
+    a.x += o[h].x;
+    a.y += o[h].y;
   }
+  reinterpret_cast<float2*>(lds + LDS_IN)[t] = a;
+  reinterpret_cast<float2*>(lds + LDS_A)[t] = a;
+  __syncthreads();
+}
+// All threads: the MLP vector (MQ_I tagged values) into LDS dst; ends with __syncthreads.
+MQ_DEV void m_input_all(const float* m, float* dst, int tag, MqSync* sy) {
+  const int t = tid();
+  constexpr int P = MQ_I / 2 / MQ_THREADS;
+  static_assert(P * 2 * MQ_THREADS == MQ_I, "whole pairs per thread");
+  tag_poll_all<P>(m, [&](int i) { return t + MQ_THREADS * i; }, tag, sy,
+                  [&](int i, float lo, float hi) {
+                    reinterpret_cast<float2*>(dst)[t + MQ_THREADS * i] = make_float2(lo, hi);
+                  });
   __syncthreads();
 }
 // Sync wave: a layer output (MQ_H / 2 pair words of `src`, epoch e) into LDS dst (and dst2).
@@ -1208,13 +1277,14 @@ MQ_DEV void input_hidden_bf16(float* lds, const bf16_t* src) {
 }
 
 // Phase boundary of the head-group kernel.  Order of the workgroup's memory operations: the
-// sync wave's output stores (waited for), its barrier arrival, then the compute waves' weight
-// prefetch, then the sync wave's barrier polls and input loads.  A workgroup's memory queue is
-// first-in first-out in practice, so arriving before the prefetch is issued keeps the arrival
-// from waiting behind tens of KB of weight loads, and the prefetch drains while the barrier
-// completes.
-// ACK = false (an exchange of epoch words, no counter arrival): the sync wave does not wait for
-// its stores to be acknowledged; readers recognise the words by their epoch.
+// sync wave's output stores (with ACK, waited for, then its barrier arrival), then the compute
+// waves' weight prefetch, then the sync wave's waits and input loads.  A workgroup's memory queue
+// is first-in first-out in practice, so publishing before the prefetch is issued keeps the
+// outputs from waiting behind tens of KB of weight loads, and the prefetch drains while the
+// exchange completes.
+// ACK = false (exchanges of epoch or tagged words, no counter arrival): the sync wave does not
+// wait for its stores to be acknowledged; readers recognise the words by their epoch.  ACK =
+// true only for the group barrier before the split-mode attention merge.
 template <bool ACK = true, class Epi, class Arrive, class Prefetch, class Wait, class Input>
 MQ_DEV void phase_step(Epi epilogue, Arrive arrive, Prefetch prefetch, Wait wait, Input input) {
   __syncthreads();
@@ -1375,7 +1445,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
     const bf16_t* cs = p.cos + (size_t)pos * MQ_D;
     const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
-    uint32_t nbar = 0, ngb = 0;
+    uint32_t ngb = 0;
     phase_step(MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
     // first K/V block of this workgroup's chunk (EARLY: stand-ins for a workgroup without one)
     const int kv0 = ga.active ? ga.p0 : 0;
@@ -1442,25 +1512,25 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       stamp(p, wg, l, 4);
       opart_run(wo, w, h, j, NG, lds);
       stamp(p, wg, l, 5);
-      // O partials -> a: every group's copy, replicated grid barrier
-      phase_step([&] {
-                   opart_publish(&x->opart[0][0][0], h, j, NG, lds);
+      // O partials -> a: tagged words in every group's copy, polled by every thread
+      phase_step<false>([&] {
+                   opart_publish(&x->opart[par][0][0][0], h, j, NG, lds, e);
                    // local mode: the new position's K/V row (ALDS_KN/VN are still intact)
                    if (ga.local && ga.has_pos) attn_cache_row(p, l, h, pos, lds);
                  },
-                 [&] { grid_barrier_arrive(sy); },
+                 MQ_NOTHING,
                  [&] { if (ga.active) gu_load(wgu, w, wg, G); },
-                 [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); }, MQ_NOTHING);
-      gu_input_all(&x->opart[copy][0][0], lds);
+                 MQ_NOTHING, MQ_NOTHING);
+      gu_input_all(&x->opart[par][copy][0][0], lds, (int)(e & 3u), sy);
       stamp(p, wg, l, 6);
       gu_run(wgu, w, wg, G, lds);
       stamp(p, wg, l, 7);
-      // silu(gate) * up -> down: every group's copy, replicated grid barrier
-      phase_step([&] { gu_publish(&x->m[0][0], wg, G, lds); },
-                 [&] { grid_barrier_arrive(sy); },
+      // silu(gate) * up -> down: tagged words in every group's copy, polled by every thread
+      phase_step<false>([&] { gu_publish(&x->m[par][0][0], wg, G, lds, e); },
+                 MQ_NOTHING,
                  [&] { down_load(wd, w, wg, G); },
-                 [&] { grid_barrier_wait(sy, (++nbar) * (uint32_t)G); },
-                 [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, x->m[copy]); });
+                 MQ_NOTHING, MQ_NOTHING);
+      m_input_all(x->m[par][copy], lds + LDS_IN, (int)(e & 3u), sy);
       stamp(p, wg, l, 8);
       down_run(wd, w, wg, G, lds);
       stamp(p, wg, l, 9);
@@ -1517,7 +1587,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
     else hidden_gather(dst, nullptr, xprev, 0, sy);
   };
   if constexpr (PH == 5) {
-    phase_sync(sy, 0, false, MQ_NOTHING, [&] {
+    phase_sync(MQ_NOTHING, [&] {
       if (p.num_layers == 0) wave_copy_bf16_1024(lds + LDS_IN, xe);
       else hidden_gather(lds + LDS_IN, nullptr, x->h[(p.num_layers - 1) & 1][0], 0, sy);
     });
@@ -1527,7 +1597,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
     if constexpr (PH == 0) {
       QkvSet ws;
       gqkv_load(ws, w, h, j, NG);
-      phase_sync(sy, 0, false, MQ_NOTHING, [&] { load_x(lds + LDS_IN); });
+      phase_sync(MQ_NOTHING, [&] { load_x(lds + LDS_IN); });
       gqkv_run(ws, w, h, j, NG, lds);
       phase_finish([&] { gqkv_publish(x->q[par][h], 0, j, NG, lds); });
     }
@@ -1538,7 +1608,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
         kv_block_load<false>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), ga.p0,
                              min(ga.p1, ga.p0 + MQ_ATT_BLOCK), pos, p.cos);
         q_operand_clear(lds);
-        phase_sync(sy, 0, false, MQ_NOTHING, [&] {
+        phase_sync(MQ_NOTHING, [&] {
           attn_input(x->q[par][h], 0, sy, w.q_norm, w.k_norm, p.cos + (size_t)pos * MQ_D,
                      p.sin + (size_t)pos * MQ_D, p.scale_log2, lds);
         });
@@ -1555,18 +1625,18 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       else
         group_merge(s->part, h, ga.nch, lds);
       opart_run(ws, w, h, j, NG, lds);
-      phase_finish([&] { opart_publish(&x->opart[0][0][0], h, j, NG, lds); });
+      phase_finish([&] { opart_publish(&x->opart[par][0][0][0], h, j, NG, lds, 0); });
     }
     if constexpr (PH == 3) {
       GateUpSet ws;
       gu_load(ws, w, wg, G);
-      phase_sync(sy, 0, false, MQ_NOTHING, [&] {
+      phase_sync(MQ_NOTHING, [&] {
         load_x(lds + LDS_HID);
         wait_all_memory();
-        gu_input(&x->opart[0][0][0], lds);
+        gu_input(&x->opart[par][0][0][0], lds);
       });
       gu_run(ws, w, wg, G, lds);
-      phase_finish([&] { gu_publish(&x->m[0][0], wg, G, lds); });
+      phase_finish([&] { gu_publish(&x->m[par][0][0], wg, G, lds, 0); });
     }
     if constexpr (PH == 4) {
       DownSet ws;
@@ -1577,9 +1647,10 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       float res = 0.f;
       if (wave_id() == MQ_SYNC_WAVE && t < nrh) {
         const float xv = l == 0 ? bf16_to_f32(xe[r0h + t]) : hidden_row(xprev, r0h + t);
-        res = a_elem(xv, &x->opart[0][0][0], r0h + t);
+        res = a_elem(xv, &x->opart[par][0][0][0], r0h + t);
       }
-      phase_sync(sy, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, x->m[0]); });
+      phase_sync(MQ_NOTHING, MQ_NOTHING);
+      m_input_all(x->m[par][0], lds + LDS_IN, -1, sy);
       down_run(ws, w, wg, G, lds);
       phase_finish([&] {
         down_publish(wg, G, lds, res, [](int, float) {});
@@ -1596,7 +1667,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_qkv_kernel(MqDecodeParams p,
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   QkvSet ws;
   qkv_load(ws, p.layers[l], blockIdx.x, gridDim.x);
-  phase_sync(&p.st->sync, 0, false, MQ_NOTHING, [&] { wave_copy_bf16_1024(lds + LDS_IN, x); });
+  phase_sync(MQ_NOTHING, [&] { wave_copy_bf16_1024(lds + LDS_IN, x); });
   qkv_run(ws, p.layers[l], blockIdx.x, gridDim.x, lds);
   phase_finish([&] { qkv_publish(p.s->qkv, blockIdx.x, gridDim.x, lds); });
 }
@@ -1605,7 +1676,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_rope_kernel(MqDecodeParams p
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   const int h = blockIdx.x;
   const MqLayerW w = p.layers[l];
-  phase_sync(&p.st->sync, 0, false, MQ_NOTHING, [&] {
+  phase_sync(MQ_NOTHING, [&] {
     attn_input_f(p.s->qkv, w.q_norm, w.k_norm, p.cos + (size_t)pos * MQ_D,
                  p.sin + (size_t)pos * MQ_D, h, p.scale_log2, lds);
   });
@@ -1648,7 +1719,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_o_kernel(MqDecodeParams p, i
   int r0, nr;
   row_range(MQ_H, blockIdx.x, gridDim.x, r0, nr);
   float res = lane_id() < nr ? bf16_to_f32(x[r0 + lane_id()]) : 0.f;
-  phase_sync(&p.st->sync, 0, false, MQ_NOTHING,
+  phase_sync(MQ_NOTHING,
              [&] { wave_copy_coh<MQ_QDIM>(lds + LDS_IN, att); });
   o_run(ws, p.layers[l], blockIdx.x, gridDim.x, lds);
   phase_finish([&] { o_publish(a_out, blockIdx.x, gridDim.x, lds, res); });
@@ -1659,7 +1730,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_gateup_kernel(MqDecodeParams
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   GateUpSet ws;
   gu_load(ws, p.layers[l], blockIdx.x, gridDim.x);
-  phase_sync(&p.st->sync, 0, false, MQ_NOTHING, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, a); });
+  phase_sync(MQ_NOTHING, [&] { wave_copy_coh<MQ_H>(lds + LDS_IN, a); });
   gu_run(ws, p.layers[l], blockIdx.x, gridDim.x, lds);
   phase_finish([&] { gu_publish_f(p.s->mlp, blockIdx.x, gridDim.x, lds); });
 }
@@ -1671,7 +1742,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_down_kernel(MqDecodeParams p
   int r0, nr;
   hid_rows(blockIdx.x, gridDim.x, r0, nr);
   float res = lane_id() < nr ? ld_coh(a + r0 + lane_id()) : 0.f;
-  phase_sync(&p.st->sync, 0, false, MQ_NOTHING,
+  phase_sync(MQ_NOTHING,
              [&] { wave_copy_coh<MQ_I>(lds + LDS_IN, p.s->mlp); });
   down_run(ws, p.layers[l], blockIdx.x, gridDim.x, lds);
   phase_finish([&] {
@@ -1685,7 +1756,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, 
                                                                int* tok_out, float* logits,
                                                                bool round_norm) {
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
-  phase_sync(&p.st->sync, 0, false, MQ_NOTHING,
+  phase_sync(MQ_NOTHING,
              [&] { wave_copy_bf16_1024(lds + LDS_IN, x); });
   lm_head_run(p, blockIdx.x, gridDim.x, lds, tok_out, logits, 0, false, round_norm);
 }
@@ -1693,7 +1764,6 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, 
 // ---------------------------------------------------------------------- state kernels
 __global__ void mq_fill_state_kernel(MqState* st, int pos, int clear_err) {
   const int t = threadIdx.x;
-  if (t < MQ_BAR_COPIES * MQ_BAR_STRIPES) st->sync.bar[t / MQ_BAR_STRIPES][t % MQ_BAR_STRIPES].v = 0;
   if (t < MQ_NKV) st->sync.attn[t].v = 0;
   if (t == 0) {
     st->sync.done.v = 0;
@@ -1774,8 +1844,7 @@ int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t st
 }
 
 int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream, bool clear_err) {
-  mq_fill_state_kernel<<<1, MQ_BAR_COPIES * MQ_BAR_STRIPES, 0, stream>>>(st, pos,
-                                                                         clear_err ? 1 : 0);
+  mq_fill_state_kernel<<<1, 64, 0, stream>>>(st, pos, clear_err ? 1 : 0);
   return launch_status();
 }
 

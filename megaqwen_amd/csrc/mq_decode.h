@@ -46,15 +46,18 @@ struct MqScratch {
 // 256; on MI355X that took a 1024-value exchange among 256 workgroups from 3.4 to 1.6 us.
 // The one-kernel-per-phase mode writes the same buffers with epoch 0 (never expected: epochs
 // start at 1) and reads the values only.  The two larger exchanges (the O partials, 8192 values,
-// and silu(gate) * up, 3072) measured no faster as epoch words than with a counter barrier whose
-// counters are replicated per group, and would not fit the sync wave's registers as one poll.
+// and silu(gate) * up, 3072) keep 4-byte words: the epoch's low two bits replace the two lowest
+// mantissa bits of each fp32 value (tag_bits in decode.hip), and every thread of the reader polls
+// its share.  Against a counter barrier (stores, acknowledgement wait, arrival atomics, poll,
+// then the data load) that took a token at pos 128 from 572 to 536 us.
 struct MqExchange {
   uint64_t q[2][MQ_NKV][4 * MQ_D];       // q|k|v rows of each kv-head group (read by the group)
   uint64_t h[2][MQ_GROUPS][MQ_H / 2];    // layer output: a bf16 row pair per word (bits 0-15
                                          // row 2k, 16-31 row 2k + 1), epoch in bits 32-63
-  // passed by counter barriers (fp32, one copy per group):
-  float opart[MQ_GROUPS][MQ_NKV][MQ_H];  // per-kv-head O-projection partials W_o[:, head h] att_h
-  float m[MQ_GROUPS][MQ_I];              // silu(gate) * up
+  // tagged fp32 words (the two low mantissa bits hold the epoch's low bits), by layer parity,
+  // one copy per group (XCD):
+  float opart[2][MQ_GROUPS][MQ_NKV][MQ_H];  // per-kv-head O-projection partials W_o[:, head h] att_h
+  float m[2][MQ_GROUPS][MQ_I];              // silu(gate) * up
 };
 MQ_DEV uint64_t xword(float v, uint32_t e) { return ((uint64_t)e << 32) | __float_as_uint(v); }
 MQ_DEV float xvalue(uint64_t w) { return __uint_as_float((uint32_t)w); }

@@ -209,8 +209,10 @@ MQ_DEV uint64_t wave_max_u64(uint64_t k) {
 // gfx950 lowers to single `sc1` loads/stores that are coherent across the 8 XCD-private L2s.
 // No release/acquire fences are used: those lower to whole-L2 writeback/invalidate
 // (buffer_wbl2 / buffer_inv) and cost ~7 us per grid barrier on MI355X.  Ordering instead comes
-// from waiting for every outstanding memory operation of the wave (s_waitcnt 0) before arriving
-// at a barrier, and from issuing the data loads only after the barrier has been observed.
+// from words that carry their own epoch (a value and its epoch are one store and one load), and,
+// for the counter barriers that remain, from waiting for every outstanding memory operation of
+// the wave (s_waitcnt 0) before arriving and issuing the data loads only after the barrier has
+// been observed.
 MQ_DEV void st_coh(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -232,7 +234,7 @@ MQ_DEV void st_coh64(uint64_t* p, uint64_t v) {
 }
 MQ_DEV void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
-// ---------------------------------------------------------------------------- grid barrier
+// ---------------------------------------------------------------------------- sync state
 // Sync state lives in its own 128-byte lines (one L2 line each on gfx950).
 struct alignas(128) MqLine {
   uint32_t v;
@@ -242,12 +244,7 @@ struct alignas(128) MqLine64 {
   unsigned long long v;
   uint32_t pad[30];
 };
-#define MQ_BAR_STRIPES 32
-#define MQ_BAR_COPIES 8
 struct MqSync {
-  MqLine bar[MQ_BAR_COPIES][MQ_BAR_STRIPES];  // grid-barrier arrival counters: every workgroup
-                               // adds to its stripe of each copy and polls copy wg % 8 (reset at
-                               // step end)
   MqLine attn[MQ_NKV];         // per-kv-head group barrier / split-K completion counters
                                // (reset at step end)
   MqLine done;                 // LM-head completion counter
@@ -259,62 +256,8 @@ struct MqSync {
 // workgroup never arrives (then `err` is set and later barriers do not wait at all).
 #define MQ_SPIN_LIMIT (1u << 23)
 
-MQ_DEV uint32_t row16_sum_u32(uint32_t v) {
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, MQ_DPP_QUAD_XOR1, 0xF, 0xF, true);
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, MQ_DPP_QUAD_XOR2, 0xF, 0xF, true);
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, MQ_DPP_ROW_HALF_MIRROR, 0xF, 0xF, true);
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, MQ_DPP_ROW_MIRROR, 0xF, 0xF, true);
-  return v;
-}
-
-// Grid-wide barrier for a co-resident (cooperative) launch, executed by the sync wave only
-// (the caller brackets it with __syncthreads).  `target` is the arrival count that completes
-// this barrier: k * gridDim.x for the k-th barrier of the step.  Workgroup w adds 1 to stripe
-// w % 32 of each of the 8 counter copies (lanes 0-7, one atomic each; the counters of a copy sit
-// in 32 separate 128-byte lines, since atomics on one line serialise) and lanes 0..31 poll the
-// 32 stripes of copy w % 8 at once and sum them with DPP, so each line is polled by 32
-// workgroups rather than 256 (measured 3.7 against 4.4 us for an 8192-value exchange among 256
-// workgroups).  The sync wave never has weight prefetches outstanding, so its polls are not
-// queued behind them (gfx9 returns a wave's loads in order).  Precondition: the stores other
-// workgroups will read after this barrier have been waited for.
-MQ_DEV void grid_barrier_arrive(MqSync* s) {
-  const int lane = __lane_id();
-  if (lane < MQ_BAR_COPIES)
-    __hip_atomic_fetch_add(&s->bar[lane][blockIdx.x % MQ_BAR_STRIPES].v, 1u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-}
-MQ_DEV void grid_barrier_wait(MqSync* s, uint32_t target) {
-  const int lane = __lane_id();
-  const int copy = blockIdx.x % MQ_BAR_COPIES;
-  uint32_t spins = 0;
-  while (true) {
-    uint32_t v = 0;
-    // the error flag (one line that every workgroup would poll) is read on every 8th poll only
-    if (lane < MQ_BAR_STRIPES)
-      v = __hip_atomic_load(&s->bar[copy][lane].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else if (lane == 63 && (spins & 7) == 0)
-      v = __hip_atomic_load(&s->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t e = __builtin_amdgcn_readlane(v, 63);
-    const uint32_t rs = row16_sum_u32(v);
-    const uint32_t total = __builtin_amdgcn_readlane(rs, 0) + __builtin_amdgcn_readlane(rs, 16);
-    if (e != 0 || (int32_t)(total - target) >= 0) break;
-    // back-off of ~128 clocks between polls: polling back to back slows down the arrivals on
-    // the stripe lines
-    __builtin_amdgcn_s_sleep(2);
-    if (++spins > MQ_SPIN_LIMIT) {
-      if (lane == 0)
-        __hip_atomic_store(&s->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
-    }
-  }
-}
-MQ_DEV void grid_barrier_wave(MqSync* s, uint32_t target) {
-  grid_barrier_arrive(s);
-  grid_barrier_wait(s, target);
-}
-
 // Barrier of one kv-head group (the NG workgroups of one XCD in the persistent kernel), executed
-// by the sync wave: arrival counter attn[h] is cumulative within a step like the grid stripes.
+// by the sync wave: arrival counter attn[h] is cumulative within a step (reset at step end).
 MQ_DEV void group_barrier_arrive(MqSync* s, int h) {
   if (__lane_id() == 0)
     __hip_atomic_fetch_add(&s->attn[h].v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
