@@ -260,7 +260,7 @@ int mq_decoder_set_position(mq_decoder* dec, int pos, void* stream) {
   if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "decoder is NULL");
   if (pos < 0 || pos > dec->p.max_seq)
     return fail(MQ_ERR_POSITION, "position %d outside [0, %d]", pos, dec->p.max_seq);
-  if (mq_launch_fill_state(dec->p.st, pos, static_cast<hipStream_t>(stream)) != 0)
+  if (mq_launch_set_position(dec->p.st, dec->p.x, pos, static_cast<hipStream_t>(stream)) != 0)
     return fail(MQ_ERR_HIP, "state update failed");
   dec->pos = pos;
   return MQ_OK;
@@ -384,7 +384,7 @@ int mq_prefill(mq_decoder* dec, const int32_t* d_tokens, int n, int32_t* d_token
   int rc = mq_launch_prefill(dec->p, dec->host_layers.data(), dec->pf, d_tokens, n, d_token_out,
                              d_logits, dec->grid, s);
   if (rc != 0) return fail(MQ_ERR_HIP, "prefill launch failed (%d)", rc);
-  if (mq_launch_fill_state(dec->p.st, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
+  if (mq_launch_set_position(dec->p.st, dec->p.x, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
   dec->pos = n;
   return MQ_OK;
 }
@@ -404,7 +404,7 @@ int mq_prefill_embeds(mq_decoder* dec, const int32_t* d_tokens, int n, const voi
                              d_logits, dec->grid, s, static_cast<const bf16_t*>(d_embeds),
                              embeds_start, embeds_len);
   if (rc != 0) return fail(MQ_ERR_HIP, "prefill launch failed (%d)", rc);
-  if (mq_launch_fill_state(dec->p.st, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
+  if (mq_launch_set_position(dec->p.st, dec->p.x, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
   dec->pos = n;
   return MQ_OK;
 }
@@ -421,7 +421,7 @@ int mq_debug_prefill_layers(mq_decoder* dec, const int32_t* d_tokens, int n,
   int rc = mq_launch_prefill(dec->p, dec->host_layers.data(), dec->pf, d_tokens, n, d_token_out,
                              d_logits, dec->grid, s, nullptr, 0, 0, static_cast<bf16_t*>(d_trace));
   if (rc != 0) return fail(MQ_ERR_HIP, "prefill launch failed (%d)", rc);
-  if (mq_launch_fill_state(dec->p.st, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
+  if (mq_launch_set_position(dec->p.st, dec->p.x, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
   dec->pos = n;
   return MQ_OK;
 }

@@ -243,17 +243,19 @@ MQ_DEV void phase_finish(Epi epilogue) {
   if (wave_id() == MQ_SYNC_WAVE) epilogue();
 }
 #define MQ_NOTHING [] {}
-// Tagged fp32 exchange words (the O-projection partials and the MLP vector): the two lowest
-// mantissa bits of each value carry the low two bits of the layer's exchange epoch, so a reader
-// polls the data itself, with no store acknowledgement, counter or separate barrier.  The buffers
-// alternate by layer parity, so the word a reader may see before the new one was written two
-// layers back (or one, across a step boundary when the layer count is odd): its epoch differs
-// by 1..2, and so do the two tag bits.  A workgroup cannot run two layers ahead of another, since
-// every layer needs every workgroup's values.  Every mode publishes and reads the same
-// truncated values (the one-kernel-per-phase mode with tag 0 and no polling), so the modes stay
-// bit-identical; the truncation is below 2^-22 relative, far under the bf16 rounding these
-// values meet downstream.
-MQ_DEV uint32_t tag_bits(float v, uint32_t e) { return (__float_as_uint(v) & ~3u) | (e & 3u); }
+// Tagged fp32 exchange words (the O-projection partials, the MLP vector and the split-mode
+// attention partials): the two lowest mantissa bits of each value carry xtag(e) = 1 + e mod 3
+// for the layer's exchange epoch e, so a reader polls the data itself, with no store
+// acknowledgement, counter or separate barrier.  The buffers alternate by layer parity and every
+// word of a buffer is rewritten in every layer of its parity (or was cleared to zero, which no
+// tag matches), so the word a reader may see before the new one was written one or two epochs
+// earlier and carries another tag.  A workgroup cannot run two layers ahead of another, since
+// every layer needs every workgroup's values.  The one-kernel-per-phase mode publishes the same
+// truncated values with the same epochs (and reads without polling), so the modes stay
+// bit-identical and either may follow the other; the truncation is below 2^-22 relative, far
+// under the bf16 rounding these values meet downstream.
+MQ_DEV uint32_t xtag(uint32_t e) { return 1u + e % 3u; }
+MQ_DEV uint32_t tag_bits(float v, uint32_t e) { return (__float_as_uint(v) & ~3u) | xtag(e); }
 MQ_DEV float untag(uint32_t u) { return __uint_as_float(u & ~3u); }
 MQ_DEV void st_tag(float* p, float v, uint32_t e) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), tag_bits(v, e), __ATOMIC_RELAXED,
@@ -749,8 +751,13 @@ MQ_DEV void attn_write_partial(float* part, int h, int c, const float* lds) {
 // by all 512 threads with every load issued up front (one memory round trip):
 //   att_j = sum_c exp2(m_c - M_j) o_c / sum_c exp2(m_c - M_j) l_c.
 // Thread t owns query head j = t / 256, dims 2*((t / 4) % 64) + {0, 1} and chunks c = t % 4 + 4i.
-template <class Out>
-MQ_DEV void attn_merge(const float* part, int h, int nch, float* lds, Out out) {
+// TAGGED: the partials are tagged words (tag_bits); with tag >= 1 every thread polls its words
+// until they carry it, with tag < 0 they are read as they are; either way the tags are removed.
+// NI: chunk words per thread (nch <= 4 NI); the group merges use 8, which keeps the persistent
+// kernel's prefetched weights and the polled words within its registers.
+template <bool TAGGED = false, int NI = 16, class Out>
+MQ_DEV void attn_merge(const float* part, int h, int nch, float* lds, Out out, int tag = -1,
+                       MqSync* sy = nullptr) {
   float* mw = lds + ALDS_MW;      // (m, l) pairs [2][64] -> weights [2][64] at +256
   float* msum = lds + ALDS_MSUM;  // [4][2][128]
   const int t = tid();
@@ -758,12 +765,51 @@ MQ_DEV void attn_merge(const float* part, int h, int nch, float* lds, Out out) {
   float* pbase = const_cast<float*>(part);
   float2 ml = make_float2(0.f, 0.f);
   const int mj = t >= nch ? 1 : 0, mc = t - mj * nch;   // (query head, chunk) of t < 2 nch
-  if (t < 2 * nch) ml = ld_coh2(part_ptr(pbase, h, mc, mj));
-  float2 o2[16];
+  float2 o2[NI];
+  if constexpr (TAGGED) {
+    auto mlw = [&] { return reinterpret_cast<const uint64_t*>(part_ptr(pbase, h, mc, mj)); };
+    auto ow = [&](int i) {
+      return reinterpret_cast<const uint64_t*>(part_ptr(pbase, h, q + 4 * i, j) + 4 + 2 * pr);
+    };
+    uint64_t wml = t < 2 * nch ? ld_coh64(mlw()) : 0ull;
+    uint64_t wo[NI];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int c = q + 4 * i;
-    o2[i] = c < nch ? ld_coh2(part_ptr(pbase, h, c, j) + 4 + 2 * pr) : make_float2(0.f, 0.f);
+    for (int i = 0; i < NI; ++i) wo[i] = q + 4 * i < nch ? ld_coh64(ow(i)) : 0ull;
+    if (tag >= 0) {
+      const uint32_t tg = (uint32_t)tag;
+      uint32_t spins = 0;
+      while (true) {
+        bool ok = t >= 2 * nch || tag_ok2(wml, tg);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) ok = ok && (q + 4 * i >= nch || tag_ok2(wo[i], tg));
+        if (__all(ok)) break;
+        uint32_t ev = 0;
+        if (lane_id() == 0 && (spins & 15) == 15)
+          ev = __hip_atomic_load(&sy->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readlane(ev, 0) != 0) break;
+        if (++spins > MQ_SPIN_LIMIT) {
+          if (lane_id() == 0)
+            __hip_atomic_store(&sy->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        if (t < 2 * nch && !tag_ok2(wml, tg)) wml = ld_coh64(mlw());
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+          if (q + 4 * i < nch && !tag_ok2(wo[i], tg)) wo[i] = ld_coh64(ow(i));
+      }
+    }
+    ml = make_float2(untag((uint32_t)wml), untag((uint32_t)(wml >> 32)));
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      o2[i] = make_float2(untag((uint32_t)wo[i]), untag((uint32_t)(wo[i] >> 32)));
+  } else {
+    if (t < 2 * nch) ml = ld_coh2(part_ptr(pbase, h, mc, mj));
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int c = q + 4 * i;
+      o2[i] = c < nch ? ld_coh2(part_ptr(pbase, h, c, j) + 4 + 2 * pr) : make_float2(0.f, 0.f);
+    }
   }
   if (t < 2 * nch) reinterpret_cast<float2*>(mw)[mj * 64 + mc] = ml;
   __syncthreads();
@@ -781,7 +827,7 @@ MQ_DEV void attn_merge(const float* part, int h, int nch, float* lds, Out out) {
   const float* wj = mw + 256 + j * 64;
   float2 s = make_float2(0.f, 0.f);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < NI; ++i) {
     const int c = q + 4 * i;
     if (c < nch) {
       s.x = fmaf(wj[c], o2[i].x, s.x);
@@ -1086,7 +1132,7 @@ MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos, int local_max, bo
     return g;
   }
   const int want = (cache_len + MQ_ATT_SLOT - 1) / MQ_ATT_SLOT;
-  const int n0 = min(min(NG, MQ_MAX_CHUNKS), want);
+  const int n0 = min(min(NG, MQ_GROUP_CHUNKS), want);
   const int clen = (cache_len + n0 - 1) / n0;
   g.nch = (cache_len + clen - 1) / clen;
   g.p0 = j * clen;
@@ -1105,25 +1151,48 @@ MQ_DEV void group_single(const float* part, int h, float* lds) {
   }
   __syncthreads();
 }
-// Sync wave, after attn_core: this chunk's partial (m, l, o) of both query heads, and the new
-// position's K/V cache row from the chunk that holds it.
-MQ_DEV void gattn_publish(const MqDecodeParams& p, int layer, int pos, int h, int j,
-                          const GAttn& g, const float* lds) {
+// Sync wave, one kernel per phase, local mode: workgroup 0's single partial (plain values, read
+// by group_single in the next kernel) and the new position's K/V cache row.
+MQ_DEV void gattn_publish_local(const MqDecodeParams& p, int layer, int pos, int h,
+                                const GAttn& g, const float* lds) {
   const int lane = lane_id();
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = lane + 64 * i, jj = t >> 7, d = t & 127;
-    st_coh(part_ptr(p.s->part, h, j, jj) + 4 + d, lds[ALDS_ORED + t]);
+    st_coh(part_ptr(p.s->part, h, 0, jj) + 4 + d, lds[ALDS_ORED + t]);
   }
   if (lane < 2) {
-    st_coh(part_ptr(p.s->part, h, j, lane), lds[ALDS_STAT + lane]);
-    st_coh(part_ptr(p.s->part, h, j, lane) + 1, lds[ALDS_STAT + 2 + lane]);
+    st_coh(part_ptr(p.s->part, h, 0, lane), lds[ALDS_STAT + lane]);
+    st_coh(part_ptr(p.s->part, h, 0, lane) + 1, lds[ALDS_STAT + 2 + lane]);
   }
   if (g.has_pos) attn_cache_row(p, layer, h, pos, lds);
 }
-// All threads: merged attention output of query heads 2h, 2h+1 into LDS_ATTH.
-MQ_DEV void group_merge(const float* part, int h, int nch, float* lds) {
-  attn_merge(part, h, nch, lds, [&](int jj, int d, float o) { lds[LDS_ATTH + jj * MQ_D + d] = o; });
+// Sync wave, after attn_core: this member's partial (m, l, o) of both query heads as tagged words
+// of epoch e into slot j of `part` (one layer-parity half of MqExchange.part), and the new
+// position's K/V cache row from the chunk that holds it.  A member without a chunk writes an
+// empty partial (m = -inf, l = 0, o = 0; never read), so that every slot is rewritten in every
+// split-mode layer, as the tags require.
+MQ_DEV void gattn_publish(const MqDecodeParams& p, int layer, int pos, int h, int j,
+                          const GAttn& g, const float* lds, float* part, uint32_t e) {
+  const int lane = lane_id();
+  if (j < MQ_GROUP_CHUNKS) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = lane + 64 * i, jj = t >> 7, d = t & 127;
+      st_tag(part_ptr(part, h, j, jj) + 4 + d, g.active ? lds[ALDS_ORED + t] : 0.f, e);
+    }
+    if (lane < 2) {
+      st_tag(part_ptr(part, h, j, lane), g.active ? lds[ALDS_STAT + lane] : -INFINITY, e);
+      st_tag(part_ptr(part, h, j, lane) + 1, g.active ? lds[ALDS_STAT + 2 + lane] : 0.f, e);
+    }
+  }
+  if (g.has_pos) attn_cache_row(p, layer, h, pos, lds);
+}
+// All threads: merged attention output of query heads 2h, 2h+1 into LDS_ATTH from tagged
+// partials (tag >= 1: polled until they carry it; tag < 0: read as they are).
+MQ_DEV void group_merge(const float* part, int h, int nch, float* lds, int tag, MqSync* sy) {
+  attn_merge<true, MQ_GROUP_CHUNKS / 4>(part, h, nch, lds,
+                   [&](int jj, int d, float o) { lds[LDS_ATTH + jj * MQ_D + d] = o; }, tag, sy);
   __syncthreads();
 }
 
@@ -1420,7 +1489,6 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
   // on one box, repeated; unchanged at pos 4096)
   if (wave_id() == MQ_SYNC_WAVE) __builtin_amdgcn_s_setprio(3);
   MqSync* sy = &p.st->sync;
-  MqScratch* s = p.s;
   MqExchange* x = p.x;
   const int copy = wg % MQ_GROUPS;        // the exchange copy this workgroup reads
   int r0h, nrh;
@@ -1445,7 +1513,6 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
     const bf16_t* cs = p.cos + (size_t)pos * MQ_D;
     const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
-    uint32_t ngb = 0;
     phase_step(MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
     // first K/V block of this workgroup's chunk (EARLY: stand-ins for a workgroup without one)
     const int kv0 = ga.active ? ga.p0 : 0;
@@ -1503,11 +1570,11 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       if (ga.active) attn_core(p, l, h, ga.p0, ga.p1, pos, ga.has_new, kv, lds, ga.local);
       stamp(p, wg, l, 3);
       if (!ga.local) {
-        phase_step([&] { if (ga.active) gattn_publish(p, l, pos, h, j, ga, lds); },
-                   [&] { group_barrier_arrive(sy, h); },
-                   [&] { opart_load(wo, w, h, j, NG); },
-                   [&] { group_barrier_wait(sy, h, (++ngb) * (uint32_t)NG); }, MQ_NOTHING);
-        group_merge(s->part, h, ga.nch, lds);
+        // chunk partials -> merge: tagged words of the group's slots, polled by every thread
+        phase_step<false>([&] { gattn_publish(p, l, pos, h, j, ga, lds, x->part[par], e); },
+                          MQ_NOTHING, [&] { opart_load(wo, w, h, j, NG); }, MQ_NOTHING,
+                          MQ_NOTHING);
+        group_merge(x->part[par], h, ga.nch, lds, (int)xtag(e), sy);
       }
       stamp(p, wg, l, 4);
       opart_run(wo, w, h, j, NG, lds);
@@ -1521,7 +1588,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
                  MQ_NOTHING,
                  [&] { if (ga.active) gu_load(wgu, w, wg, G); },
                  MQ_NOTHING, MQ_NOTHING);
-      gu_input_all(&x->opart[par][copy][0][0], lds, (int)(e & 3u), sy);
+      gu_input_all(&x->opart[par][copy][0][0], lds, (int)xtag(e), sy);
       stamp(p, wg, l, 6);
       gu_run(wgu, w, wg, G, lds);
       stamp(p, wg, l, 7);
@@ -1530,7 +1597,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
                  MQ_NOTHING,
                  [&] { down_load(wd, w, wg, G); },
                  MQ_NOTHING, MQ_NOTHING);
-      m_input_all(x->m[par][copy], lds + LDS_IN, (int)(e & 3u), sy);
+      m_input_all(x->m[par][copy], lds + LDS_IN, (int)xtag(e), sy);
       stamp(p, wg, l, 8);
       down_run(wd, w, wg, G, lds);
       stamp(p, wg, l, 9);
@@ -1578,8 +1645,14 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
   const int h = wg % MQ_GROUPS, j = wg / MQ_GROUPS, NG = G / MQ_GROUPS;
   const int par = l & 1;
   const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
-  // exchange words of this mode carry epoch 0: written by a completed earlier kernel, they are
-  // read without waiting (copy 0 of the grid-wide buffers)
+  // the (value, epoch) words of this mode carry epoch 0: written by a completed earlier kernel,
+  // they are read without waiting (copy 0 of the grid-wide buffers).  Its tagged words carry the
+  // epoch the persistent kernel would give this layer (xep + l + 1; the LM-head kernel advances
+  // xep by num_layers), so a persistent launch after steps of this mode never finds a stale
+  // tagged word whose two tag bits match its expected epoch.
+  const uint32_t et = __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(&p.st->xep.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) +
+      (uint32_t)l + 1u;
   const uint64_t* xprev = x->h[(l + 1) & 1][0];   // layer l - 1's output
   // the layer input: the embedding row for layer 0, else the previous layer's output
   auto load_x = [&](float* dst) {
@@ -1591,7 +1664,9 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       if (p.num_layers == 0) wave_copy_bf16_1024(lds + LDS_IN, xe);
       else hidden_gather(lds + LDS_IN, nullptr, x->h[(p.num_layers - 1) & 1][0], 0, sy);
     });
-    lm_head_run(p, wg, G, lds, p.tok_out, p.logits, pos, true);
+    // et - 1 = xep: the step's epochs were xep + 1 .. xep + num_layers
+    lm_head_run(p, wg, G, lds, p.tok_out, p.logits, pos, true, false, false, 0, true,
+                et - 1u + (uint32_t)p.num_layers);
   } else {
     const MqLayerW w = p.layers[l];
     if constexpr (PH == 0) {
@@ -1613,7 +1688,13 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
                      p.sin + (size_t)pos * MQ_D, p.scale_log2, lds);
         });
         attn_core(p, l, h, ga.p0, ga.p1, pos, ga.has_new, kv, lds);
-        phase_finish([&] { gattn_publish(p, l, pos, h, j, ga, lds); });
+        phase_finish([&] {
+          if (ga.local) gattn_publish_local(p, l, pos, h, ga, lds);
+          else gattn_publish(p, l, pos, h, j, ga, lds, x->part[par], et);
+        });
+      } else if (!ga.local) {
+        // no chunk: the slot is still rewritten (an empty partial), as in the persistent kernel
+        phase_finish([&] { gattn_publish(p, l, pos, h, j, ga, lds, x->part[par], et); });
       }
     }
     if constexpr (PH == 2) {
@@ -1623,9 +1704,9 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       if (ga.local)
         group_single(s->part, h, lds);
       else
-        group_merge(s->part, h, ga.nch, lds);
+        group_merge(x->part[par], h, ga.nch, lds, -1, sy);
       opart_run(ws, w, h, j, NG, lds);
-      phase_finish([&] { opart_publish(&x->opart[par][0][0][0], h, j, NG, lds, 0); });
+      phase_finish([&] { opart_publish(&x->opart[par][0][0][0], h, j, NG, lds, et); });
     }
     if constexpr (PH == 3) {
       GateUpSet ws;
@@ -1636,7 +1717,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
         gu_input(&x->opart[par][0][0][0], lds);
       });
       gu_run(ws, w, wg, G, lds);
-      phase_finish([&] { gu_publish(&x->m[par][0][0], wg, G, lds, 0); });
+      phase_finish([&] { gu_publish(&x->m[par][0][0], wg, G, lds, et); });
     }
     if constexpr (PH == 4) {
       DownSet ws;
@@ -1852,6 +1933,12 @@ int mq_launch_clear_state(MqState* st, MqExchange* x, hipStream_t stream) {
   const int rc = mq_launch_zero(x, sizeof(MqExchange), stream);
   if (rc != 0) return rc;
   return mq_launch_fill_state(st, 0, stream, true);
+}
+
+int mq_launch_set_position(MqState* st, MqExchange* x, int pos, hipStream_t stream) {
+  const int rc = mq_launch_zero(&x->part[0][0], sizeof(x->part), stream);
+  if (rc != 0) return rc;
+  return mq_launch_fill_state(st, pos, stream);
 }
 
 int mq_launch_zero(void* ptr, size_t bytes, hipStream_t stream) {

@@ -20,6 +20,7 @@
 #define MQ_SYNC_WAVE 7
 
 #define MQ_MAX_CHUNKS 64                // attention split-K chunks per kv head (upper bound)
+#define MQ_GROUP_CHUNKS 32              // split-K chunks of one kv-head group (decode kernel)
 #define MQ_MAX_LAYERS 64                // decoder layers (the persistent kernel keeps their
                                         // weight-pointer table in LDS)
 #define MQ_STEPS_PER_LAUNCH 64          // decode_steps: tokens chained inside one persistent launch

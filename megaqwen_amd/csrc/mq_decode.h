@@ -58,6 +58,11 @@ struct MqExchange {
   // one copy per group (XCD):
   float opart[2][MQ_GROUPS][MQ_NKV][MQ_H];  // per-kv-head O-projection partials W_o[:, head h] att_h
   float m[2][MQ_GROUPS][MQ_I];              // silu(gate) * up
+  // split-mode attention partials (m, l, o[128] per query head and chunk, part_ptr layout), tagged
+  // words by layer parity; every member of a group rewrites its slot in every split-mode layer.
+  // Cleared whenever the position is set: a sequence that starts in local mode and reaches split
+  // mode later must not find an earlier sequence's words there, whose tags may match.
+  float part[2][MQ_NKV * MQ_MAX_CHUNKS * MQ_GQA * MQ_PART_STRIDE];
 };
 MQ_DEV uint64_t xword(float v, uint32_t e) { return ((uint64_t)e << 32) | __float_as_uint(v); }
 MQ_DEV float xvalue(uint64_t w) { return __uint_as_float((uint32_t)w); }
@@ -144,6 +149,9 @@ __host__ __device__ inline int mq_decode_early_kv(int pos, int grid, int local_m
 // (sticky until mq_decoder_reset or creation, so mq_decoder_check still reports it) unless
 // `clear_err`.
 int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream, bool clear_err = false);
+// A new position for the next decode step (after a prefill or a caller's seek): clears the
+// split-mode attention partials, then sets the state as mq_launch_fill_state does.
+int mq_launch_set_position(MqState* st, MqExchange* x, int pos, hipStream_t stream);
 // Creation / reset: the state as above with the error flag and the exchange epoch zeroed, and the
 // exchange buffers cleared (no stale word can carry an epoch a later step expects).
 int mq_launch_clear_state(MqState* st, MqExchange* x, hipStream_t stream);

@@ -315,6 +315,35 @@ def test_multi_step_launch_matches_single_steps(small):
     dec.check()
 
 
+def test_mode_switches_without_reset(small):
+    """Steps of the one-kernel-per-phase mode between persistent ones, with no reset in between.
+    The tagged exchange words (O partials, MLP vector) of that mode carry the persistent kernel's
+    epoch sequence, and its LM-head kernel advances the device epoch count by the layer count, so
+    a persistent step that follows never takes a word left by the other mode for a fresh one.
+    Tokens and logits equal an all-persistent run bit for bit; with 2 layers per step the switches
+    land on every residue of the epoch count mod 4.  A chained launch after mixed steps too."""
+    dec, _, sp, _ = small
+    first = int(make_tokens(1, sp["vocab_size"], seed=21)[0])
+    dec.set_mode("persistent")
+    dec.reset()
+    ref_t, ref_l, t = [], [], first
+    for _ in range(28):
+        t, lg = dec.decode_step_with_logits(t)
+        ref_t.append(t)
+        ref_l.append(lg.clone())
+    pattern = ("mmmppmpppmmpmpmmmppppmpm")
+    dec.reset()
+    t = first
+    for i, m in enumerate(pattern):
+        dec.set_mode("multi_kernel" if m == "m" else "persistent")
+        t, lg = dec.decode_step_with_logits(t)
+        assert t == ref_t[i] and torch.equal(lg, ref_l[i]), (i, m)
+    dec.set_mode("persistent")
+    chain = dec.decode_steps_cuda(t, 4).cpu().tolist()
+    assert chain == ref_t[len(pattern):len(pattern) + 4]
+    dec.check()
+
+
 def test_decode_greedy_cuda_eos(small):
     dec, _, sp, _ = small
     first = int(make_tokens(1, sp["vocab_size"], seed=7)[0])
