@@ -4,16 +4,17 @@
 //   P1  RMSNorm(x) and the fused q|k|v GEMV (4096 rows x 1024)
 //   P2  per-(kv head, position chunk) attention: q/k RMSNorm + RoPE prologue, K/V cache write of
 //       the new position, two-pass softmax over the chunk; with several chunks per head each
-//       publishes a split-K partial (m, l, o[128]) and the last chunk to finish merges them
+//       publishes a split-K partial (m, l, o[128]), merged by every workgroup that needs the
+//       head's output
 //   P3  O GEMV (1024 x 2048) + residual
 //   P4  RMSNorm(a) + gate/up GEMVs (2 x 3072 x 1024) + silu(g) * u
 //   P5  down GEMV (1024 x 3072) + residual, rounded to bf16 (the layer output)
 //   LM  final RMSNorm + LM-head GEMV (vocab x 1024) + argmax (packed 64-bit atomic max)
 // The phases run either inside one persistent cooperative kernel, which hands data between
-// workgroups through device-coherent exchange words that carry the layer's epoch (no grid
-// barrier at all; one kv-head-group barrier per layer above 176 cache positions, against 225
-// grid.sync() per token in the reference's ldg_decode_kernel,
-// csrc/megakernel/fused_decode_ldg_kernel.inl:5-259), or as one kernel launch per phase.
+// workgroups through device-coherent exchange words that carry the layer's epoch (no barrier
+// between workgroups at all, against 225 grid.sync() per token in the reference's
+// ldg_decode_kernel, csrc/megakernel/fused_decode_ldg_kernel.inl:5-259), or as one kernel launch
+// per phase.
 //
 // Workgroup organisation (512 threads): waves 0..6 are compute waves, wave 7 is the sync wave.
 // Per phase the compute waves finish their dot products; the sync wave publishes the outputs with
@@ -1031,8 +1032,6 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
     }
     if (__builtin_amdgcn_readlane(old, 0) == (uint32_t)G - 1) {
       // the last workgroup: token, then the step's sync state cleared
-      if (lane < MQ_NKV)
-        __hip_atomic_store(&sy->attn[lane].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (lane == 0) {
         const unsigned long long kk =
             __hip_atomic_load(&sy->argmax.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1067,16 +1066,17 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
 //   1. q|k|v: group h computes the 512 rows of its kv head (q heads 2h, 2h+1, k and v of h),
 //      published as (value, epoch) words read by the group.
 //   2. attention split over the group's workgroups by position chunks, partials (m, l, o)
-//      published per chunk.
-//   3. group barrier; every workgroup of the group merges the partials (att of its two query
-//      heads) and computes its rows of the O projection restricted to the head's 256 columns,
+//      published per chunk as tagged words (an empty partial from a workgroup without a chunk).
+//   3. every workgroup of the group polls and merges the partials (att of its two query heads)
+//      and computes its rows of the O projection restricted to the head's 256 columns,
 //      published as tagged words to every group's copy.
 //   4. a = x + sum_h opart_h (every thread polls its rows), RMSNorm, gate|up rows; silu(g) * u
 //      published as tagged words.
 //   5. down rows + a -> bf16 layer output, published as (bf16 pair, epoch) words -> next layer.
-// That is 4 exchanges and no grid-wide barrier per layer.  For short contexts (cache length
-// <= attn_local_max) steps 2-3 collapse: every workgroup of the group attends over all
-// positions itself (its O rows prefetched with the K/V rows), and the group barrier goes away.
+// That is 5 exchanges (4 for short contexts) and no barrier per layer.  For short contexts
+// (cache length <= attn_local_max) steps 2-3 collapse: every workgroup of the group attends over
+// all positions itself (its O rows prefetched with the K/V rows), and the partial exchange goes
+// away.
 // Measured per layer (MFMA scores, epoch-word exchanges): at 128 positions local mode takes
 // 18.7 us against 19.2 us split; at 200 positions 19.7 against 19.6, so the default switches
 // to split chunks above 176 positions.
@@ -1346,26 +1346,20 @@ MQ_DEV void input_hidden_bf16(float* lds, const bf16_t* src) {
 }
 
 // Phase boundary of the head-group kernel.  Order of the workgroup's memory operations: the
-// sync wave's output stores (with ACK, waited for, then its barrier arrival), then the compute
-// waves' weight prefetch, then the sync wave's waits and input loads.  A workgroup's memory queue
-// is first-in first-out in practice, so publishing before the prefetch is issued keeps the
-// outputs from waiting behind tens of KB of weight loads, and the prefetch drains while the
-// exchange completes.
-// ACK = false (exchanges of epoch or tagged words, no counter arrival): the sync wave does not
-// wait for its stores to be acknowledged; readers recognise the words by their epoch.  ACK =
-// true only for the group barrier before the split-mode attention merge.
-template <bool ACK = true, class Epi, class Arrive, class Prefetch, class Wait, class Input>
-MQ_DEV void phase_step(Epi epilogue, Arrive arrive, Prefetch prefetch, Wait wait, Input input) {
+// sync wave's output stores, then the compute waves' weight prefetch, then the sync wave's input
+// loads (polled where the input is an epoch-word exchange; the tagged exchanges are polled by
+// every thread after this returns).  A workgroup's memory queue is first-in first-out in
+// practice, so publishing before the prefetch is issued keeps the outputs from waiting behind
+// tens of KB of weight loads, and the prefetch drains while the exchange completes.  The sync
+// wave does not wait for its stores to be acknowledged: readers recognise the words by their
+// epoch or tag, so no store needs to land before another.
+template <class Epi, class Prefetch, class Input>
+MQ_DEV void phase_step(Epi epilogue, Prefetch prefetch, Input input) {
   __syncthreads();
-  if (wave_id() == MQ_SYNC_WAVE) {
-    epilogue();
-    if constexpr (ACK) wait_all_memory();
-    arrive();
-  }
+  if (wave_id() == MQ_SYNC_WAVE) epilogue();
   __syncthreads();
   if (wave_id() < MQ_CWAVES) prefetch();
   if (wave_id() == MQ_SYNC_WAVE) {
-    wait();
     input();
     wait_all_memory();
   }
@@ -1374,7 +1368,7 @@ MQ_DEV void phase_step(Epi epilogue, Arrive arrive, Prefetch prefetch, Wait wait
 
 // ------------------------------------------------------------------------------- kernels
 // Reads and validates the step's position and input token.  The result is identical in every
-// workgroup, so an invalid step makes all of them return before the first barrier.
+// workgroup, so an invalid step makes all of them return before the first exchange.
 MQ_DEV bool step_inputs(const MqDecodeParams& p, const int* tok_in, int& pos, int& tok) {
   // uniform by construction; readfirstlane lets the compiler treat everything derived from them
   // as scalar (uniform branches, no per-lane copies of alternative code paths)
@@ -1452,7 +1446,7 @@ MQ_DEV void step_wait(const MqDecodeParams& p, uint32_t target) {
       const uint32_t e = __builtin_amdgcn_readlane(v, 63);
       const uint32_t c = __builtin_amdgcn_readlane(v, 0);
       if (e != 0 || (int32_t)(c - target) >= 0) break;
-      __builtin_amdgcn_s_sleep(2);   // back-off, as in the grid barrier
+      __builtin_amdgcn_s_sleep(2);   // back-off between polls
       if (++spins > MQ_SPIN_LIMIT) {
         if (lane == 0)
           __hip_atomic_store(&p.st->sync.err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1465,8 +1459,8 @@ MQ_DEV void step_wait(const MqDecodeParams& p, uint32_t target) {
 
 // EARLY: the long-context variant (chosen per launch by the host, MqDecodeParams.early_kv): a
 // layer's K rows are issued right after its q|k|v weights, one phase earlier than otherwise, so
-// they stream in during the q|k|v dot products and the group barrier; its V rows follow at the
-// q|k|v barrier.  Both K/V loads have a fixed instruction count (kv_block_load_all), so the
+// they stream in during the q|k|v dot products and exchange; its V rows follow at the q|k|v
+// exchange.  Both K/V loads have a fixed instruction count (kv_block_load_all), so the
 // compiler waits for the q|k|v weights alone.  The variant is correct at any position: steps
 // where a workgroup has no chunk load a stand-in K row and ignore it (and issue their gate|up
 // weights at the q|k|v boundary, as in the other variant), and chunks of <= 8 positions use the
@@ -1484,7 +1478,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     __syncthreads();
   }
   const int h = wg % MQ_GROUPS, j = wg / MQ_GROUPS, NG = G / MQ_GROUPS;
-  // the sync wave's instructions (barrier polls, exchange loads and stores) win issue arbitration
+  // the sync wave's instructions (exchange polls, loads and stores) win issue arbitration
   // over the compute waves' weight prefetches: 576.7 against 579.5 us per token at pos 128 (A/B
   // on one box, repeated; unchanged at pos 4096)
   if (wave_id() == MQ_SYNC_WAVE) __builtin_amdgcn_s_setprio(3);
@@ -1513,7 +1507,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
     const bf16_t* cs = p.cos + (size_t)pos * MQ_D;
     const bf16_t* sn = p.sin + (size_t)pos * MQ_D;
-    phase_step(MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
+    phase_step(MQ_NOTHING, MQ_NOTHING, [&] { input_hidden_bf16(lds, xe); });
     // first K/V block of this workgroup's chunk (EARLY: stand-ins for a workgroup without one)
     const int kv0 = ga.active ? ga.p0 : 0;
     const int kv1 = ga.active ? min(ga.p1, ga.p0 + MQ_ATT_BLOCK) : 0;
@@ -1538,8 +1532,8 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       // critical path).  Workgroups with a chunk issue its K/V rows here instead: issued before
       // the q|k|v dot products (whose loads are conditional), they made the compiler's wait for
       // the q|k|v weights wait for them too.
-      phase_step<false>(
-          [&] { gqkv_publish(x->q[par][h], e, j, NG, lds); }, MQ_NOTHING,
+      phase_step(
+          [&] { gqkv_publish(x->q[par][h], e, j, NG, lds); },
           [&] {
             if constexpr (EARLY) {
               // a workgroup without a chunk (some cache lengths below ~990 leave the last one
@@ -1561,7 +1555,6 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
               }
             }
           },
-          MQ_NOTHING,
           [&] {
             if (ga.active)
               attn_input(x->q[par][h], e, sy, w.q_norm, w.k_norm, cs, sn, p.scale_log2, lds);
@@ -1571,51 +1564,45 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       stamp(p, wg, l, 3);
       if (!ga.local) {
         // chunk partials -> merge: tagged words of the group's slots, polled by every thread
-        phase_step<false>([&] { gattn_publish(p, l, pos, h, j, ga, lds, x->part[par], e); },
-                          MQ_NOTHING, [&] { opart_load(wo, w, h, j, NG); }, MQ_NOTHING,
-                          MQ_NOTHING);
+        phase_step([&] { gattn_publish(p, l, pos, h, j, ga, lds, x->part[par], e); },
+                   [&] { opart_load(wo, w, h, j, NG); }, MQ_NOTHING);
         group_merge(x->part[par], h, ga.nch, lds, (int)xtag(e), sy);
       }
       stamp(p, wg, l, 4);
       opart_run(wo, w, h, j, NG, lds);
       stamp(p, wg, l, 5);
       // O partials -> a: tagged words in every group's copy, polled by every thread
-      phase_step<false>([&] {
+      phase_step([&] {
                    opart_publish(&x->opart[par][0][0][0], h, j, NG, lds, e);
                    // local mode: the new position's K/V row (ALDS_KN/VN are still intact)
                    if (ga.local && ga.has_pos) attn_cache_row(p, l, h, pos, lds);
                  },
-                 MQ_NOTHING,
-                 [&] { if (ga.active) gu_load(wgu, w, wg, G); },
-                 MQ_NOTHING, MQ_NOTHING);
+                 [&] { if (ga.active) gu_load(wgu, w, wg, G); }, MQ_NOTHING);
       gu_input_all(&x->opart[par][copy][0][0], lds, (int)xtag(e), sy);
       stamp(p, wg, l, 6);
       gu_run(wgu, w, wg, G, lds);
       stamp(p, wg, l, 7);
       // silu(gate) * up -> down: tagged words in every group's copy, polled by every thread
-      phase_step<false>([&] { gu_publish(&x->m[par][0][0], wg, G, lds, e); },
-                 MQ_NOTHING,
-                 [&] { down_load(wd, w, wg, G); },
-                 MQ_NOTHING, MQ_NOTHING);
+      phase_step([&] { gu_publish(&x->m[par][0][0], wg, G, lds, e); },
+                 [&] { down_load(wd, w, wg, G); }, MQ_NOTHING);
       m_input_all(x->m[par][copy], lds + LDS_IN, (int)xtag(e), sy);
       stamp(p, wg, l, 8);
       down_run(wd, w, wg, G, lds);
       stamp(p, wg, l, 9);
       // layer output -> next layer (or the LM head): epoch words
-      phase_step<false>(
+      phase_step(
           [&] {
             float res = lane_id() < nrh ? lds[LDS_A + r0h + lane_id()] : 0.f;
             down_publish(wg, G, lds, res, [](int, float) {});
             hidden_publish(p, l, r0h, nrh, res, e);
           },
-          MQ_NOTHING,
           [&] {
             if (l + 1 < p.num_layers) {
               gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG);
               if constexpr (EARLY) k_early(l + 1);
             }
           },
-          MQ_NOTHING, [&] { hidden_gather(lds + LDS_IN, lds + LDS_HID, x->h[par][copy], e, sy); });
+          [&] { hidden_gather(lds + LDS_IN, lds + LDS_HID, x->h[par][copy], e, sy); });
       stamp(p, wg, l, 10);
     }
     const bool more = step + 1 < p.nsteps;
@@ -1845,7 +1832,6 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, 
 // ---------------------------------------------------------------------- state kernels
 __global__ void mq_fill_state_kernel(MqState* st, int pos, int clear_err) {
   const int t = threadIdx.x;
-  if (t < MQ_NKV) st->sync.attn[t].v = 0;
   if (t == 0) {
     st->sync.done.v = 0;
     if (clear_err) {

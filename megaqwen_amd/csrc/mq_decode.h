@@ -37,19 +37,22 @@ struct MqScratch {
 };
 
 // Exchange buffers of the decode kernels (in the caller's workspace).  Values that cross
-// workgroups without a counter barrier travel as 64-bit (value, epoch) words: the low 32 bits are
+// workgroups travel without any barrier.  The q|k|v rows and the layer output are 64-bit
+// (value, epoch) words: the low 32 bits are
 // the fp32 value, the high 32 bits the exchange epoch of the step and layer that wrote it.  A
 // reader polls the words it needs until every one carries the epoch it expects: one store and one
 // load per value, no acknowledgement wait before an arrival and no atomic.  The buffers
 // alternate by layer parity.  Values every workgroup reads are written once per kv-head group
 // (copy g is read by the workgroups wg % 8 == g), so each cache line has 32 readers instead of
 // 256; on MI355X that took a 1024-value exchange among 256 workgroups from 3.4 to 1.6 us.
-// The one-kernel-per-phase mode writes the same buffers with epoch 0 (never expected: epochs
-// start at 1) and reads the values only.  The two larger exchanges (the O partials, 8192 values,
-// and silu(gate) * up, 3072) keep 4-byte words: the epoch's low two bits replace the two lowest
-// mantissa bits of each fp32 value (tag_bits in decode.hip), and every thread of the reader polls
-// its share.  Against a counter barrier (stores, acknowledgement wait, arrival atomics, poll,
-// then the data load) that took a token at pos 128 from 572 to 536 us.
+// The one-kernel-per-phase mode writes these with epoch 0 (never expected: epochs start at 1)
+// and reads the values only.  The larger exchanges (the O partials, 8192 values, silu(gate) * up,
+// 3072, and the split-mode attention partials) keep 4-byte words: a tag derived from the epoch
+// replaces the two lowest mantissa bits of each fp32 value (tag_bits in decode.hip), and every
+// thread of the reader polls its share; both modes write them with the same epochs.  Against a
+// counter barrier (stores, acknowledgement wait, arrival atomics, poll, then the data load) that
+// took a token at pos 128 from 572 to 536 us, and the tagged attention partials a token at 1024
+// positions from 620 to 579 us.
 struct MqExchange {
   uint64_t q[2][MQ_NKV][4 * MQ_D];       // q|k|v rows of each kv-head group (read by the group)
   uint64_t h[2][MQ_GROUPS][MQ_H / 2];    // layer output: a bf16 row pair per word (bits 0-15
@@ -99,7 +102,7 @@ struct MqDecodeParams {
   float scale_log2;            // log2(e) / sqrt(D): scores are kept in the log2 domain
   int attn_local_max;          // cache lengths up to this are attended over all positions by
                                // every workgroup of a kv-head group (no split-K partials, no
-                               // merge barrier); longer ones are split into position chunks
+                               // merge); longer ones are split into position chunks
   int early_kv;                // persistent mode: launch the long-context variant that issues
                                // each layer's K rows with its q|k|v weights (host-chosen per
                                // launch, mq_decode_early_kv; correct at any position)
@@ -109,8 +112,7 @@ struct MqDecodeParams {
 };
 
 // Per-layer timestamps of the persistent kernel's debug mode (s_memrealtime, 100 MHz):
-// 0 layer start, then for each of the 5 phases k: 2k+1 compute done (stores waited for),
-// 2k+2 barrier passed.
+// 0 layer start, then for each of the 5 phases k: 2k+1 compute done, 2k+2 input received.
 #define MQ_NSTAMP 11
 
 // Attention work split: number of position chunks per kv head for a given cache length and
@@ -145,7 +147,7 @@ __host__ __device__ inline int mq_decode_early_kv(int pos, int grid, int local_m
   const int cache_len = pos + 1;
   return cache_len >= (grid / MQ_GROUPS) * MQ_ATT_SLOT && cache_len > local_max ? 1 : 0;
 }
-// Clears the barrier / completion state and sets the device position; the error flag is kept
+// Clears the completion state and sets the device position; the error flag is kept
 // (sticky until mq_decoder_reset or creation, so mq_decoder_check still reports it) unless
 // `clear_err`.
 int mq_launch_fill_state(MqState* st, int pos, hipStream_t stream, bool clear_err = false);

@@ -210,9 +210,9 @@ MQ_DEV uint64_t wave_max_u64(uint64_t k) {
 // No release/acquire fences are used: those lower to whole-L2 writeback/invalidate
 // (buffer_wbl2 / buffer_inv) and cost ~7 us per grid barrier on MI355X.  Ordering instead comes
 // from words that carry their own epoch (a value and its epoch are one store and one load), and,
-// for the counter barriers that remain, from waiting for every outstanding memory operation of
-// the wave (s_waitcnt 0) before arriving and issuing the data loads only after the barrier has
-// been observed.
+// for the one counter that remains (the LM head's completion count, which ends a step), from
+// waiting for every outstanding memory operation of the wave (s_waitcnt 0) before the arrival
+// atomic and issuing the dependent loads only after the count has been observed.
 MQ_DEV void st_coh(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -245,39 +245,12 @@ struct alignas(128) MqLine64 {
   uint32_t pad[30];
 };
 struct MqSync {
-  MqLine attn[MQ_NKV];         // per-kv-head group barrier / split-K completion counters
-                               // (reset at step end)
   MqLine done;                 // LM-head completion counter
-  MqLine err;                  // nonzero after a barrier timed out or a bound was violated
+  MqLine err;                  // nonzero after a wait timed out or a bound was violated
   MqLine64 argmax;             // packed (value, index) key of the running vocabulary argmax
 };
 
-// Spin bound: every wave leaves a barrier after at most this many polls even if some
-// workgroup never arrives (then `err` is set and later barriers do not wait at all).
+// Spin bound: every wave leaves a wait (an exchange poll) after at most this many polls even if
+// some workgroup never publishes (then `err` is set and later waits end at once).
 #define MQ_SPIN_LIMIT (1u << 23)
 
-// Barrier of one kv-head group (the NG workgroups of one XCD in the persistent kernel), executed
-// by the sync wave: arrival counter attn[h] is cumulative within a step (reset at step end).
-MQ_DEV void group_barrier_arrive(MqSync* s, int h) {
-  if (__lane_id() == 0)
-    __hip_atomic_fetch_add(&s->attn[h].v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-MQ_DEV void group_barrier_wait(MqSync* s, int h, uint32_t target) {
-  const int lane = __lane_id();
-  uint32_t spins = 0;
-  while (true) {
-    uint32_t v = 0;
-    if (lane == 0)
-      v = __hip_atomic_load(&s->attn[h].v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else if (lane == 63)
-      v = __hip_atomic_load(&s->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t e = __builtin_amdgcn_readlane(v, 63);
-    const uint32_t c = __builtin_amdgcn_readlane(v, 0);
-    if (e != 0 || (int32_t)(c - target) >= 0) break;
-    if (++spins > MQ_SPIN_LIMIT) {
-      if (lane == 0)
-        __hip_atomic_store(&s->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
-    }
-  }
-}

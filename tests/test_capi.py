@@ -85,3 +85,21 @@ def test_decoder_requires_cuda_tensors():
     t = torch.zeros(4, dtype=torch.bfloat16)
     with pytest.raises((TypeError, ValueError)):
         MegakernelDecoder(t, [t] * 11, t, t, t, t, 1, 16)
+
+
+def test_decode_kernels_do_not_spill():
+    """The decode kernels' register budget (two waves per SIMD for the 512-thread persistent
+    kernel) is nearly full; a spill to scratch compiles silently and slows every decode step
+    (a merge that held 16 64-bit words per thread spilled 99 VGPRs and cost ~15%).  The build records the
+    compiler's per-kernel resource usage; every decode kernel must show no spill and no scratch."""
+    from megaqwen_amd.build import RESOURCE_REPORT, parse_resource_usage
+    if not os.path.exists(RESOURCE_REPORT):
+        pytest.skip("no resource report: build with `python -m megaqwen_amd.build`")
+    usage = parse_resource_usage(open(RESOURCE_REPORT).read())
+    persistent = [k for k in usage if "mq_decode_persistent_kernel" in k]
+    assert len(persistent) == 2, sorted(usage)
+    for name, u in usage.items():
+        assert u.get("VGPRs Spill", -1) == 0, (name, u)
+        assert u.get("ScratchSize", -1) == 0, (name, u)
+    for name in persistent:
+        assert usage[name]["VGPRs"] + usage[name].get("AGPRs", 0) <= 256, usage[name]
