@@ -137,6 +137,31 @@ def time_bucket(dec, start_pos: int, steps: int, per_launch_steps: int = STEPS_P
     return wall, per_launch, steps / len(chunks)
 
 
+def time_prefill_fused(dec, n: int, reps: int):
+    """Best event-timed `mq_prefill_fused` call over `reps` (the fused short-prompt prefill of
+    MegakernelFusedPrefillDecoder, n <= 64), after one warm-up call."""
+    import torch
+    from megaqwen_amd.synthetic import make_tokens
+    d = make_tokens(n, 151936, seed=1).cuda()
+    times = []
+    for r in range(reps + 1):
+        dec.reset()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        rc = dec._lib.mq_prefill_fused(dec._h, d.data_ptr(), n, None, 0, 0,
+                                       dec._tok.data_ptr() + 4, None,
+                                       torch.cuda.current_stream().cuda_stream)
+        b.record()
+        if rc != 0:
+            raise RuntimeError(dec._lib.mq_last_error().decode())
+        torch.cuda.synchronize()
+        if r > 0:
+            times.append(a.elapsed_time(b) / 1e3)
+    dec.check()
+    return min(times)
+
+
 def time_prefill(dec, n: int, reps: int):
     import torch
     from megaqwen_amd.synthetic import make_tokens
@@ -474,11 +499,14 @@ def main():
                "tflops": round(prefill_flops(512) / pf_mean / 1e12, 1),
                "ms_4096": round(pf4_best * 1e3, 2),
                "mfma_util_4096": round(prefill_flops(4096) / pf4_best / MFMA_BF16_PEAK, 4),
-               "ms_16": round(pf16_best * 1e3, 3), "ms_64": round(pf64_best * 1e3, 3)}
+               "ms_16": round(pf16_best * 1e3, 3), "ms_64": round(pf64_best * 1e3, 3),
+               "fused_ms_16": round(time_prefill_fused(dec, 16, 5) * 1e3, 3),
+               "fused_ms_64": round(time_prefill_fused(dec, 64, 5) * 1e3, 3)}
     print(f"[bench] prefill 512: {prefill['ms']} ms, {prefill['tok_s']} tok/s, "
           f"{prefill['tflops']} TFLOP/s = {prefill['mfma_util'] * 100:.1f}% of dense bf16 peak; "
           f"4096: {prefill['ms_4096']} ms ({prefill['mfma_util_4096'] * 100:.1f}%); 16: "
-          f"{prefill['ms_16']} ms; 64: {prefill['ms_64']} ms",
+          f"{prefill['ms_16']} ms; 64: {prefill['ms_64']} ms; fused prefill 16: "
+          f"{prefill['fused_ms_16']} ms, 64: {prefill['fused_ms_64']} ms",
           file=sys.stderr, flush=True)
     head = res[128]
     achieved = head["bytes_per_token"] * head["tokens_per_launch"] / (head["launch_us"] * 1e-6)

@@ -173,6 +173,20 @@ int mq_prefill_embeds(mq_decoder* dec, const int32_t* d_tokens, int n, const voi
                       int embeds_start, int embeds_len, int32_t* d_token_out, float* d_logits,
                       void* stream);
 
+/* prefill_step / prefill_asr of MegakernelFusedPrefillDecoder (bindings_fused_prefill.cpp:235-330)
+ * over the reference's prefill megakernel (prefill_megakernel, fused_prefill_megakernel_core.inl:
+ * 658-745, launched by fused_prefill_megakernel_launch.inl): one cooperative launch runs all
+ * layers over the n prompt positions with fp32 activations (bf16 weights and K/V cache rows, no
+ * bf16 rounding of the residual stream), then the final norm and LM head of the last position.
+ * 1 <= n <= min(64, max_prefill_len).  d_embeds (bf16 [embeds_len, 1024]) may be NULL, then
+ * embeds_len must be 0; otherwise rows [embeds_start, embeds_start + embeds_len) take it, with
+ * the checks of mq_prefill_embeds.  Writes the greedy next token (and the fp32 logits if
+ * d_logits is non-NULL) and sets the position to n.  MQ_ERR_UNSUPPORTED on a device that cannot
+ * hold 256 co-resident 512-thread workgroups. */
+int mq_prefill_fused(mq_decoder* dec, const int32_t* d_tokens, int n, const void* d_embeds,
+                     int embeds_start, int embeds_len, int32_t* d_token_out, float* d_logits,
+                     void* stream);
+
 /* Debug hook: mq_prefill that also writes the residual stream after every layer to d_trace
  * (bf16 [num_layers][n][hidden_size]), for layer-by-layer parity checks of the prefill path
  * (launch_prefill_float's per-layer hidden_bf16, fused_prefill_launch.inl:245-657). */

@@ -29,7 +29,7 @@ EXPORTED = (
     "mq_abi_version", "mq_last_error", "mq_workspace_bytes", "mq_kv_cache_bytes",
     "mq_decoder_create", "mq_decoder_destroy", "mq_decoder_reset", "mq_decoder_position",
     "mq_decoder_set_host_position", "mq_decoder_set_position", "mq_decoder_set_mode", "mq_decoder_get_mode", "mq_decoder_grid", "mq_decode_step",
-    "mq_decode_steps", "mq_debug_decode_step_layers", "mq_debug_decode_step_timing", "mq_decoder_check", "mq_prefill", "mq_prefill_embeds", "mq_debug_prefill_layers", "mq_debug_prefill_buffers", "mq_op_qkv_rope", "mq_op_attention", "mq_op_attention_noalloc",
+    "mq_decode_steps", "mq_debug_decode_step_layers", "mq_debug_decode_step_timing", "mq_decoder_check", "mq_prefill", "mq_prefill_embeds", "mq_prefill_fused", "mq_debug_prefill_layers", "mq_debug_prefill_buffers", "mq_op_qkv_rope", "mq_op_attention", "mq_op_attention_noalloc",
     "mq_op_mlp", "mq_op_decode_layer", "mq_op_lm_head", "mq_flash_attn_workspace_bytes",
     "mq_flash_attn_bhwd",
 )
@@ -92,6 +92,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "mq_decoder_check": (I, [P, P]),
         "mq_prefill": (I, [P, P, I, P, P, P]),
         "mq_prefill_embeds": (I, [P, P, I, P, I, I, P, P, P]),
+        "mq_prefill_fused": (I, [P, P, I, P, I, I, P, P, P]),
         "mq_debug_prefill_layers": (I, [P, P, I, P, P, P, P]),
         "mq_debug_prefill_buffers": (I, [P, ctypes.POINTER(P)]),
         "mq_op_qkv_rope": (I, [P, I, P, I, P, P]),

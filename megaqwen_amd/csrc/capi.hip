@@ -37,7 +37,7 @@ int fail(int code, const char* fmt, ...) {
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct Layout {
-  size_t state, layers, scratch, xch, prefill, total;
+  size_t state, layers, scratch, xch, prefill, fused, total;
 };
 
 Layout layout_of(const mq_model_desc* d) {
@@ -47,7 +47,9 @@ Layout layout_of(const mq_model_desc* d) {
   L.scratch = align_up(L.layers + sizeof(MqLayerW) * (size_t)d->num_layers, 256);
   L.xch = align_up(L.scratch + sizeof(MqScratch), 256);
   L.prefill = align_up(L.xch + sizeof(MqExchange), 256);
-  L.total = align_up(L.prefill + mq_prefill_workspace_bytes(d->max_prefill_len), 256);
+  L.fused = align_up(L.prefill + mq_prefill_workspace_bytes(d->max_prefill_len), 256);
+  // the fused short-prompt prefill's fp32 buffers (only for decoders that can prefill)
+  L.total = align_up(L.fused + (d->max_prefill_len > 0 ? mq_fused_workspace_bytes() : 0), 256);
   return L;
 }
 
@@ -109,6 +111,7 @@ struct mq_decoder {
   size_t kv_bytes;
   char* ws;
   MqPrefillBuffers pf;
+  MqFusedArgs fused;
   std::vector<MqLayerW> host_layers;
 };
 
@@ -219,6 +222,8 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   dec->kv_bytes = (size_t)desc->num_layers * MQ_NKV * (size_t)desc->max_seq_len * MQ_D * 2;
   dec->ws = ws;
   mq_prefill_bind(&dec->pf, ws + lay.prefill, desc->max_prefill_len);
+  memset(&dec->fused, 0, sizeof(dec->fused));
+  if (desc->max_prefill_len > 0) mq_fused_bind(&dec->fused, ws + lay.fused);
   if (mq_launch_clear_state(p.st, p.x, nullptr) != 0 ||
       (dec->pf.cnt != nullptr && mq_launch_zero(dec->pf.cnt, dec->pf.cnt_bytes, nullptr) != 0) ||
       hipStreamSynchronize(nullptr) != hipSuccess) {
@@ -405,6 +410,42 @@ int mq_prefill_embeds(mq_decoder* dec, const int32_t* d_tokens, int n, const voi
                              embeds_start, embeds_len);
   if (rc != 0) return fail(MQ_ERR_HIP, "prefill launch failed (%d)", rc);
   if (mq_launch_set_position(dec->p.st, dec->p.x, n, s) != 0) return fail(MQ_ERR_HIP, "state update failed");
+  dec->pos = n;
+  return MQ_OK;
+}
+
+int mq_prefill_fused(mq_decoder* dec, const int32_t* d_tokens, int n, const void* d_embeds,
+                     int embeds_start, int embeds_len, int32_t* d_token_out, float* d_logits,
+                     void* stream) {
+  if (dec == nullptr || d_tokens == nullptr || d_token_out == nullptr)
+    return fail(MQ_ERR_INVALID_ARG, "decoder and token pointers must be non-NULL");
+  if (n <= 0) return fail(MQ_ERR_INVALID_ARG, "Empty input sequence");
+  if (n > dec->max_prefill || n > MQ_FUSED_MAX_N)
+    return fail(MQ_ERR_INVALID_ARG, "Prefill sequence length %d exceeds maximum %d", n,
+                dec->max_prefill < MQ_FUSED_MAX_N ? dec->max_prefill : MQ_FUSED_MAX_N);
+  if (d_embeds != nullptr) {
+    if (embeds_len <= 0) return fail(MQ_ERR_INVALID_ARG, "audio_embeds must have audio_len > 0");
+    if (embeds_start < 0 || embeds_start + embeds_len > n)
+      return fail(MQ_ERR_INVALID_ARG, "Invalid audio_start_idx/audio_len for the given seq_len");
+  } else if (embeds_len != 0) {
+    return fail(MQ_ERR_INVALID_ARG, "embeds_len without embeddings");
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  MqFusedArgs f = dec->fused;
+  f.tokens = d_tokens;
+  f.n = n;
+  f.patch = static_cast<const bf16_t*>(d_embeds);
+  f.patch_start = d_embeds != nullptr ? embeds_start : 0;
+  f.patch_len = d_embeds != nullptr ? embeds_len : 0;
+  f.tok_out = d_token_out;
+  f.logits = d_logits;
+  const int rc = mq_launch_prefill_fused(dec->p, f, dec->grid, s);
+  if (rc == -2 || rc == -3)
+    return fail(MQ_ERR_UNSUPPORTED, "the fused prefill needs 256 co-resident workgroups (%d)",
+                dec->grid);
+  if (rc != 0) return fail(MQ_ERR_HIP, "fused prefill launch failed (%d)", rc);
+  if (mq_launch_set_position(dec->p.st, dec->p.x, n, s) != 0)
+    return fail(MQ_ERR_HIP, "state update failed");
   dec->pos = n;
   return MQ_OK;
 }

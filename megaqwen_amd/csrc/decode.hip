@@ -1829,6 +1829,417 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, 
   lm_head_run(p, blockIdx.x, gridDim.x, lds, tok_out, logits, 0, false, round_norm);
 }
 
+// --------------------------------------------------------- fused short-prompt prefill
+// The reference's prefill megakernel (prefill_megakernel, fused_prefill_megakernel_core.inl:
+// 658-745, behind MegakernelFusedPrefillDecoder, bindings_fused_prefill.cpp:235-330): one
+// cooperative launch runs every layer over all n <= 64 prompt positions with fp32 activations
+// (bf16 weights, bf16 K/V cache rows, no rounding of the residual stream), then the final norm
+// and the LM head of the last position.
+// Here 256 workgroups x 512 threads run five stages per layer, separated by grid barriers:
+//   q|k|v GEMM (input RMSNorm folded in) -> attention per (kv head, 16-query block): q/k RMSNorm,
+//   RoPE, K/V cache rows, causal softmax -> O GEMM + residual -> gate|up GEMM (post RMSNorm
+//   folded in) + silu(g) * u -> down GEMM + residual.
+// A GEMM stage gives a workgroup one tile of 16 output columns: its 16 weight rows are loaded
+// into registers before the barrier that precedes the stage, and all n rows of the fp32 input
+// are read with device-coherent loads after it.  Products run on v_mfma_f32_16x16x32_bf16 with
+// the fp32 input split into three bf16 parts (hi + mid + lo represent it exactly), so each
+// product is the exact product of the fp32 value and the bf16 weight, accumulated in fp32.
+// The RMSNorm of a GEMM input is folded in: the MFMAs take x * w_norm and the epilogue scales
+// each row by rsqrt(mean(x^2) + eps), which the same pass accumulates.
+#define FP_STRIPES 32                    // barrier counter stripes, one 128-byte line each
+#define FPA_S 132                        // padded row stride (floats) of the attention tiles
+#define FP_LDS_FLOATS (160 * FPA_S + 32 * 64 + 64)
+static_assert(FP_LDS_FLOATS >= 2 * 8 * 4 * 256 + 8 * 64, "GEMM partials fit the attention carve");
+static_assert(FP_LDS_FLOATS >= MQ_LDS_FLOATS, "the LM head's LDS layout fits");
+
+// Grid barrier over the launch: every thread's stores complete before the workgroup arrives at
+// one of 32 counter stripes; lanes 0-31 of wave 0 poll all stripes until their sum reaches
+// `target` (the stripes start at zero, cleared by the launcher; counts stay far below 2^24, so
+// the float sum is exact).  Loads after the barrier are issued after the poll returns.
+// LOADS: vector loads this thread issued after its last store (the next stage's weight tile,
+// fp_tile_load); vmcnt counts loads and stores together and in issue order, so waiting for
+// vmcnt <= LOADS completes the stores while the weights stay in flight.
+template <int LOADS = 0>
+MQ_DEV void fp_grid_sync(uint32_t* bar, uint32_t target, MqSync* sy) {
+  static_assert(LOADS >= 0 && LOADS < 64, "vmcnt range");
+  // s_waitcnt vmcnt(LOADS) expcnt(7) lgkmcnt(15): only the vector memory counter
+  __builtin_amdgcn_s_waitcnt((LOADS & 15) | ((LOADS >> 4) << 14) | (7 << 4) | (15 << 8));
+  __syncthreads();
+  if (wave_id() == 0) {
+    const int lane = lane_id();
+    if (lane == 0)
+      __hip_atomic_fetch_add(bar + (blockIdx.x % FP_STRIPES) * 32, 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t spins = 0;
+    while (true) {
+      uint32_t v = 0;
+      if (lane < FP_STRIPES)
+        v = __hip_atomic_load(bar + lane * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (wave_sum((float)v) >= (float)target) break;
+      uint32_t ev = 0;
+      if (lane == 0 && (spins & 15) == 15)
+        ev = __hip_atomic_load(&sy->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_amdgcn_readlane(ev, 0) != 0) break;
+      if (++spins > MQ_SPIN_LIMIT) {
+        if (lane == 0)
+          __hip_atomic_store(&sy->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  __syncthreads();
+}
+
+// 16 weight rows (row0 .. row0 + 15, K bf16 each) as the B operand of the tile's MFMAs: wave w
+// holds the 32-wide k-steps w, w + 8, ...; lane l holds row l % 16, k-dims 8 (l / 16) .. + 8.
+template <int K>
+struct FpTile {
+  uint4 b[K / 256];
+};
+template <int K>
+MQ_DEV void fp_tile_load(FpTile<K>& t, const bf16_t* row0) {
+  // after every store of the stage (fp_grid_sync counts these loads as the last ones issued)
+  asm volatile("" ::: "memory");
+  const int lane = lane_id(), wave = wave_id();
+  const bf16_t* r = row0 + (size_t)(lane & 15) * K + 8 * (lane >> 4);
+#pragma unroll
+  for (int j = 0; j < K / 256; ++j) t.b[j] = ld_nt16(r + 32 * (wave + 8 * j));
+}
+
+// x = hi + mid + lo exactly, each part bf16: v_cvt_pk_bf16_f32 rounds to nearest even, and each
+// remainder is exact in fp32 (the leading part takes the top 8 significant bits, the next the
+// following 8, the last the rest).
+typedef float mq_f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 mq_bf16x2_t __attribute__((ext_vector_type(2)));
+MQ_DEV void split3_bf16(const float (&x)[8], mq_bf16x8_t& hi, mq_bf16x8_t& mid, mq_bf16x8_t& lo) {
+  uint32_t h[4], m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const mq_f32x2_t v = {x[2 * i], x[2 * i + 1]};
+    const mq_bf16x2_t a = __builtin_convertvector(v, mq_bf16x2_t);
+    const mq_f32x2_t r = v - __builtin_convertvector(a, mq_f32x2_t);
+    const mq_bf16x2_t b = __builtin_convertvector(r, mq_bf16x2_t);
+    const mq_bf16x2_t c = __builtin_convertvector(r - __builtin_convertvector(b, mq_f32x2_t),
+                                                  mq_bf16x2_t);
+    h[i] = __builtin_bit_cast(uint32_t, a);
+    m[i] = __builtin_bit_cast(uint32_t, b);
+    l[i] = __builtin_bit_cast(uint32_t, c);
+  }
+  hi = bf16x8_of(make_uint4(h[0], h[1], h[2], h[3]));
+  mid = bf16x8_of(make_uint4(m[0], m[1], m[2], m[3]));
+  lo = bf16x8_of(make_uint4(l[0], l[1], l[2], l[3]));
+}
+
+// One GEMM tile: C[r][c] = sum_k A[r][k] (* w_norm[k]) * W[c][k] for rows r < n of the fp32
+// input A (row stride K, device-coherent) and the NT weight tiles, then epi(row, col, v[NT])
+// for every row < n and the tile's 16 columns.  With NORM the values are scaled by the row's
+// rsqrt(mean(A[r]^2) + eps) (the RMSNorm with weight w_norm).  All 512 threads take part.
+template <int K, bool NORM, int NT, class Epi>
+MQ_DEV void fp_gemm(const float* A, int n, const bf16_t* w_norm, const FpTile<K> (&t)[NT],
+                    float* lds, Epi epi) {
+  const int lane = lane_id(), wave = wave_id();
+  const int nb = (n + 15) >> 4;
+  // per-wave partials [NT][8 waves][4 blocks][16 rows][16 cols] and row sums [8][64]: C element
+  // i of lane l is (row 4 (l / 16) + i, column l % 16) of the block
+  float* part = lds;
+  float* rs = lds + NT * 8 * 4 * 256;
+  // 16-row blocks in batches of BB: all of a batch's input loads of this wave are issued before
+  // the first is used (one memory round trip per batch; the loads are device-coherent and slow
+  // to return).  Two blocks per batch for K = 1024 measured no faster than one at 64 positions
+  // (4.39 against 4.32 ms per prefill): the time goes to the volume of those loads, every
+  // workgroup reading all n input rows, not to their round trips.
+  constexpr int BB = 1;
+  for (int b0 = 0; b0 < nb; b0 += BB) {
+    // keeps the next batch's loads from being hoisted into this one (they would pin registers)
+    asm volatile("" ::: "memory");
+    uint64_t u[BB][K / 256][4];
+#pragma unroll
+    for (int sb = 0; sb < BB; ++sb) {
+      const int row = 16 * (b0 + sb) + (lane & 15);
+#pragma unroll
+      for (int j = 0; j < K / 256; ++j) {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(
+            A + (size_t)row * K + 32 * (wave + 8 * j) + 8 * (lane >> 4));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) u[sb][j][i] = row < n ? ld_coh64(src + i) : 0ull;
+      }
+    }
+#pragma unroll
+    for (int sb = 0; sb < BB; ++sb) {
+      const int bb = b0 + sb;
+      if (bb >= nb) break;
+      mq_f32x4_t c[NT];
+#pragma unroll
+      for (int q = 0; q < NT; ++q) c[q] = mq_f32x4_t{0.f, 0.f, 0.f, 0.f};
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < K / 256; ++j) {
+        const int k0 = 32 * (wave + 8 * j) + 8 * (lane >> 4);
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[2 * i] = __uint_as_float((uint32_t)u[sb][j][i]);
+          x[2 * i + 1] = __uint_as_float((uint32_t)(u[sb][j][i] >> 32));
+        }
+        if constexpr (NORM) {
+          float wn[8];
+          unpack8(ld16(w_norm + k0), wn);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            ss = fmaf(x[e], x[e], ss);
+            x[e] *= wn[e];
+          }
+        }
+        mq_bf16x8_t hi, mid, lo;
+        split3_bf16(x, hi, mid, lo);
+#pragma unroll
+        for (int q = 0; q < NT; ++q) {
+          const mq_bf16x8_t b = bf16x8_of(t[q].b[j]);
+          c[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, c[q], 0, 0, 0);
+          c[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, c[q], 0, 0, 0);
+          c[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, c[q], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < NT; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          part[((q * 8 + wave) * 4 + bb) * 256 + (4 * (lane >> 4) + i) * 16 + (lane & 15)] =
+              c[q][i];
+      if constexpr (NORM) {
+        const float sr = sum_xor32(sum_xor16(ss));   // the four lanes of row l % 16
+        if (lane < 16) rs[wave * 64 + 16 * bb + lane] = sr;
+      }
+    }
+  }
+  __syncthreads();
+  for (int idx = tid(); idx < nb * 256; idx += MQ_THREADS) {
+    const int bb = idx >> 8, e = idx & 255, row = 16 * bb + (e >> 4), col = e & 15;
+    if (row >= n) continue;
+    float r = 1.f;
+    if constexpr (NORM) {
+      float s = 0.f;
+#pragma unroll
+      for (int w8 = 0; w8 < 8; ++w8) s += rs[w8 * 64 + row];
+      r = rsqrtf(s * (1.0f / K) + MQ_EPS);
+    }
+    float v[NT];
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+      float a = 0.f;
+#pragma unroll
+      for (int w8 = 0; w8 < 8; ++w8) a += part[((q * 8 + w8) * 4 + bb) * 256 + e];
+      v[q] = NORM ? a * r : a;
+    }
+    epi(row, col, v);
+  }
+  __syncthreads();
+}
+
+// One row (128 dims, lane l: dims 2l, 2l + 1) of q or k: per-head RMSNorm with weight pair
+// `w2`, then rotate-half RoPE at position `pos` (prefill_mk_qk_norm_rope_cache,
+// fused_prefill_megakernel_core.inl:186-325): o_d = x_d c_d - x_{d+64} s_d for d < 64,
+// o_d = x_{d-64} s_d + x_d c_d otherwise; the partner dims sit in lane l ^ 32.
+MQ_DEV float2 fp_norm_rope(float2 x, uint32_t w2, const MqDecodeParams& p, int pos) {
+  const int lane = lane_id();
+  const float sc = rsqrtf(wave_sum(x.x * x.x + x.y * x.y) * (1.0f / MQ_D) + MQ_EPS);
+  const float n0 = x.x * sc * bf16_lo(w2), n1 = x.y * sc * bf16_hi(w2);
+  const float2 s0 = swap32(n0), s1 = swap32(n1);
+  const float p0 = lane < 32 ? s0.y : s0.x, p1 = lane < 32 ? s1.y : s1.x;
+  const uint32_t c2 = ld32(p.cos + (size_t)pos * MQ_D + 2 * lane);
+  const uint32_t s2 = ld32(p.sin + (size_t)pos * MQ_D + 2 * lane);
+  if (lane < 32)
+    return make_float2(n0 * bf16_lo(c2) - p0 * bf16_lo(s2), n1 * bf16_hi(c2) - p1 * bf16_hi(s2));
+  return make_float2(p0 * bf16_lo(s2) + n0 * bf16_lo(c2), p1 * bf16_hi(s2) + n1 * bf16_hi(c2));
+}
+
+// Attention item (kv head h, query block qb = positions 16 qb .. 16 qb + 15) of layer `layer`
+// (prefill_mk_causal_attention, fused_prefill_megakernel_core.inl:328-414): both query heads
+// 2h, 2h + 1 of the block against keys 0 .. min(n, 16 qb + 16) - 1, fp32 throughout (the keys
+// normalised and rotated here from the raw q|k|v rows; the block's own positions' K/V rows are
+// also written to the bf16 cache).  Scores use the reference's scale and expf softmax.
+MQ_DEV void fp_attention(const MqDecodeParams& p, const MqFusedArgs& f, const MqLayerW& w,
+                         int layer, int h, int qb, float* lds) {
+  float* Ks = lds;                       // [64][FPA_S] keys after norm + RoPE
+  float* Vs = lds + 64 * FPA_S;          // [64][FPA_S] values
+  float* Qs = lds + 128 * FPA_S;         // [32][FPA_S] rows r = 2 (i - q0) + (query head - 2h)
+  float* Ps = lds + 160 * FPA_S;         // [32][64] softmax weights
+  float* Ls = Ps + 32 * 64;              // [32] 1 / sum of the weights
+  const int n = f.n, q0 = 16 * qb, kn = min(n, q0 + 16), qn = kn - q0;
+  const int lane = lane_id(), wave = wave_id();
+  constexpr int QKV = MQ_QDIM + 2 * MQ_KVDIM;
+  const uint32_t kw = ld32(w.k_norm + 2 * lane), qw = ld32(w.q_norm + 2 * lane);
+  bf16_t* kc = p.kc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
+  bf16_t* vc = p.vc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
+  for (int j = wave; j < kn; j += MQ_WAVES) {
+    const float* row = f.qkv + (size_t)j * QKV;
+    const float2 kr = ld_coh2(row + MQ_QDIM + h * MQ_D + 2 * lane);
+    const float2 vr = ld_coh2(row + MQ_QDIM + MQ_KVDIM + h * MQ_D + 2 * lane);
+    const float2 k = fp_norm_rope(kr, kw, p, j);
+    reinterpret_cast<float2*>(Ks + j * FPA_S)[lane] = k;
+    reinterpret_cast<float2*>(Vs + j * FPA_S)[lane] = vr;
+    if (j >= q0) {
+      reinterpret_cast<uint32_t*>(kc + (size_t)j * MQ_D)[lane] =
+          (uint32_t)f32_to_bf16(k.x) | ((uint32_t)f32_to_bf16(k.y) << 16);
+      reinterpret_cast<uint32_t*>(vc + (size_t)j * MQ_D)[lane] =
+          (uint32_t)f32_to_bf16(vr.x) | ((uint32_t)f32_to_bf16(vr.y) << 16);
+    }
+  }
+  for (int r = wave; r < 2 * qn; r += MQ_WAVES) {
+    const int i = q0 + (r >> 1), hq = 2 * h + (r & 1);
+    const float2 qr = ld_coh2(f.qkv + (size_t)i * QKV + hq * MQ_D + 2 * lane);
+    reinterpret_cast<float2*>(Qs + r * FPA_S)[lane] = fp_norm_rope(qr, qw, p, i);
+  }
+  __syncthreads();
+  // scores: 16 threads per row r (a 16-lane DPP row), keys jj, jj + 16, jj + 32, jj + 48
+  const int r = tid() >> 4, jj = tid() & 15, i = q0 + (r >> 1);
+  const float scale = rsqrtf((float)MQ_D);
+  float s[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int j = jj + 16 * m;
+    s[m] = -INFINITY;
+    if (r < 2 * qn && j < kn && j <= i) {
+      float acc = 0.f;
+      const float4* qv = reinterpret_cast<const float4*>(Qs + r * FPA_S);
+      const float4* kv = reinterpret_cast<const float4*>(Ks + j * FPA_S);
+#pragma unroll 8
+      for (int d4 = 0; d4 < MQ_D / 4; ++d4) {
+        const float4 a = qv[d4], b = kv[d4];
+        acc = fmaf(a.x, b.x, acc);
+        acc = fmaf(a.y, b.y, acc);
+        acc = fmaf(a.z, b.z, acc);
+        acc = fmaf(a.w, b.w, acc);
+      }
+      s[m] = acc * scale;
+    }
+  }
+  const float mx = row16_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+  float lsum = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const float e = s[m] == -INFINITY ? 0.f : expf(s[m] - mx);
+    Ps[r * 64 + jj + 16 * m] = e;
+    lsum += e;
+  }
+  lsum = row16_sum(lsum);
+  if (jj == 0) Ls[r] = 1.0f / lsum;
+  __syncthreads();
+  // P.V: thread (r, jj) owns dims 8 jj .. 8 jj + 7 of row r
+  if (r < 2 * qn) {
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j <= i; ++j) {
+      const float pw = Ps[r * 64 + j];
+      const float4 v0 = reinterpret_cast<const float4*>(Vs + j * FPA_S + 8 * jj)[0];
+      const float4 v1 = reinterpret_cast<const float4*>(Vs + j * FPA_S + 8 * jj)[1];
+      o[0] = fmaf(pw, v0.x, o[0]);
+      o[1] = fmaf(pw, v0.y, o[1]);
+      o[2] = fmaf(pw, v0.z, o[2]);
+      o[3] = fmaf(pw, v0.w, o[3]);
+      o[4] = fmaf(pw, v1.x, o[4]);
+      o[5] = fmaf(pw, v1.y, o[5]);
+      o[6] = fmaf(pw, v1.z, o[6]);
+      o[7] = fmaf(pw, v1.w, o[7]);
+    }
+    const float inv = Ls[r];
+    float* dst = f.att + (size_t)i * MQ_QDIM + (2 * h + (r & 1)) * MQ_D + 8 * jj;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2)
+      st_coh64(reinterpret_cast<uint64_t*>(dst + e),
+               (uint64_t)__float_as_uint(o[e] * inv) |
+                   ((uint64_t)__float_as_uint(o[e + 1] * inv) << 32));
+  }
+  __syncthreads();
+}
+
+__global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodeParams p,
+                                                                      MqFusedArgs f) {
+  __shared__ __align__(16) float lds[FP_LDS_FLOATS];
+  const int wg = blockIdx.x, G = gridDim.x, n = f.n, t = tid();
+  MqSync* sy = &p.st->sync;
+  uint32_t nbar = 0;
+  // LOADS: the weight-tile loads issued since the stage's last store, when `loaded`
+  auto grid_sync = [&](auto loads, bool loaded) {
+    constexpr int L = decltype(loads)::value;
+    if (loaded)
+      fp_grid_sync<L>(f.bar, (uint32_t)G * ++nbar, sy);
+    else
+      fp_grid_sync<0>(f.bar, (uint32_t)G * ++nbar, sy);
+  };
+  using std::integral_constant;
+  constexpr int QKV = MQ_QDIM + 2 * MQ_KVDIM;
+  // embedding rows (prefill_mk_embedding, fused_prefill_megakernel_core.inl:3-33; the audio
+  // rows as the kernel's patch step, :693-703); a token id outside the vocabulary reads row 0
+  // and sets the error flag to 2
+  for (int row = wg; row < n; row += G) {
+    const int pr = row - f.patch_start;
+    const bool patched = pr >= 0 && pr < f.patch_len;
+    int tok = patched ? 0 : f.tokens[row];
+    if (tok < 0 || tok >= p.vocab) {
+      if (t == 0) __hip_atomic_store(&sy->err.v, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      tok = 0;
+    }
+    const bf16_t* src = patched ? f.patch + (size_t)pr * MQ_H : p.embed + (size_t)tok * MQ_H;
+    const uint32_t v = ld32(src + 2 * t);
+    st_coh64(reinterpret_cast<uint64_t*>(f.h + (size_t)row * MQ_H) + t,
+             (uint64_t)__float_as_uint(bf16_lo(v)) | ((uint64_t)__float_as_uint(bf16_hi(v)) << 32));
+  }
+  const int nb = (n + 15) >> 4;
+  FpTile<MQ_H> tq[1];
+  const bool q_tile = wg < QKV / 16;
+  if (p.num_layers > 0 && q_tile) fp_tile_load(tq[0], qkv_row(p.layers[0], 16 * wg));
+  grid_sync(integral_constant<int, MQ_H / 256>(), p.num_layers > 0 && q_tile);
+  for (int l = 0; l < p.num_layers; ++l) {
+    const MqLayerW w = p.layers[l];
+    // q|k|v (prefill_mk_rmsnorm + prefill_mk_qkv_projection, :35-184)
+    if (wg < QKV / 16)
+      fp_gemm<MQ_H, true, 1>(f.h, n, w.in_ln, tq, lds, [&](int row, int col, const float* v) {
+        st_coh(f.qkv + (size_t)row * QKV + 16 * wg + col, v[0]);
+      });
+    grid_sync(integral_constant<int, 0>(), false);
+    if (wg < MQ_NKV * nb) fp_attention(p, f, w, l, wg % MQ_NKV, wg / MQ_NKV, lds);
+    FpTile<MQ_QDIM> to[1];
+    if (wg < MQ_H / 16) fp_tile_load(to[0], w.wo + (size_t)16 * wg * MQ_QDIM);
+    grid_sync(integral_constant<int, MQ_QDIM / 256>(), wg < MQ_H / 16);
+    // O projection + residual (prefill_mk_o_proj_residual, :417-472)
+    if (wg < MQ_H / 16)
+      fp_gemm<MQ_QDIM, false, 1>(f.att, n, nullptr, to, lds, [&](int row, int col, const float* v) {
+        float* hp = f.h + (size_t)row * MQ_H + 16 * wg + col;
+        st_coh(hp, ld_coh(hp) + v[0]);
+      });
+    FpTile<MQ_H> tgu[2];
+    if (wg < MQ_I / 16) {
+      fp_tile_load(tgu[0], w.wg + (size_t)16 * wg * MQ_H);
+      fp_tile_load(tgu[1], w.wu + (size_t)16 * wg * MQ_H);
+    }
+    grid_sync(integral_constant<int, 2 * MQ_H / 256>(), wg < MQ_I / 16);
+    // post RMSNorm + gate|up + silu(g) * u (prefill_mk_mlp_gate_up, :474-544)
+    if (wg < MQ_I / 16)
+      fp_gemm<MQ_H, true, 2>(f.h, n, w.post_ln, tgu, lds, [&](int row, int col, const float* v) {
+        const float g = v[0], u = v[1];
+        st_coh(f.m + (size_t)row * MQ_I + 16 * wg + col, g / (1.0f + expf(-g)) * u);
+      });
+    FpTile<MQ_I> td[1];
+    if (wg < MQ_H / 16) fp_tile_load(td[0], w.wd + (size_t)16 * wg * MQ_I);
+    grid_sync(integral_constant<int, MQ_I / 256>(), wg < MQ_H / 16);
+    // down projection + residual (prefill_mk_mlp_down_residual, :546-599)
+    if (wg < MQ_H / 16)
+      fp_gemm<MQ_I, false, 1>(f.m, n, nullptr, td, lds, [&](int row, int col, const float* v) {
+        float* hp = f.h + (size_t)row * MQ_H + 16 * wg + col;
+        st_coh(hp, ld_coh(hp) + v[0]);
+      });
+    if (l + 1 < p.num_layers && q_tile) fp_tile_load(tq[0], qkv_row(p.layers[l + 1], 16 * wg));
+    grid_sync(integral_constant<int, MQ_H / 256>(), l + 1 < p.num_layers && q_tile);
+  }
+  // final RMSNorm of the last position (fp32, prefill_mk_final_norm, :601-650) + LM head argmax
+  const float2 hv = ld_coh2(f.h + (size_t)(n - 1) * MQ_H + 2 * t);
+  lds[LDS_IN + 2 * t] = hv.x;
+  lds[LDS_IN + 2 * t + 1] = hv.y;
+  __syncthreads();
+  lm_head_run(p, wg, G, lds, f.tok_out, f.logits, n - 1, false, false);
+}
+
 // ---------------------------------------------------------------------- state kernels
 __global__ void mq_fill_state_kernel(MqState* st, int pos, int clear_err) {
   const int t = threadIdx.x;
@@ -1886,6 +2297,43 @@ int mq_decode_grid(int mode, int* grid_out) {
 
 static int launch_status() {
   hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : -(int)e - 1000;
+}
+
+size_t mq_fused_workspace_bytes() {
+  return (size_t)MQ_FUSED_MAX_N * (MQ_H + MQ_QDIM + 2 * MQ_KVDIM + MQ_QDIM + MQ_I) * 4 +
+         FP_STRIPES * 128;
+}
+void mq_fused_bind(MqFusedArgs* f, char* base) {
+  float* q = reinterpret_cast<float*>(base);
+  f->h = q;
+  f->qkv = f->h + MQ_FUSED_MAX_N * MQ_H;
+  f->att = f->qkv + MQ_FUSED_MAX_N * (MQ_QDIM + 2 * MQ_KVDIM);
+  f->m = f->att + MQ_FUSED_MAX_N * MQ_QDIM;
+  f->bar = reinterpret_cast<uint32_t*>(f->m + MQ_FUSED_MAX_N * MQ_I);
+}
+static int g_fused_blocks_per_cu = -1;
+int mq_launch_prefill_fused(const MqDecodeParams& p, const MqFusedArgs& f, int grid,
+                            hipStream_t stream) {
+  if (device_info() != 0) return -1;
+  if (g_fused_blocks_per_cu < 0) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &nb, reinterpret_cast<const void*>(mq_prefill_fused_kernel), MQ_THREADS, 0) !=
+        hipSuccess)
+      nb = 0;
+    g_fused_blocks_per_cu = nb;
+  }
+  if (!g_coop_ok || g_fused_blocks_per_cu < 1 || grid > g_cu_count * g_fused_blocks_per_cu)
+    return -2;
+  if (grid < 256 || f.n < 1 || f.n > MQ_FUSED_MAX_N) return -3;
+  const int rc = mq_launch_zero(f.bar, FP_STRIPES * 128, stream);
+  if (rc != 0) return rc;
+  MqDecodeParams pc = p;
+  MqFusedArgs fc = f;
+  void* args[] = {&pc, &fc};
+  hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mq_prefill_fused_kernel),
+                                            dim3(grid), dim3(MQ_THREADS), args, 0, stream);
   return e == hipSuccess ? 0 : -(int)e - 1000;
 }
 

@@ -140,6 +140,29 @@ __host__ __device__ inline int mq_attn_chunk_len(int cache_len, int nch) {
 #endif
 
 int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t stream);
+
+// Fused short-prompt prefill (mq_prefill_fused_kernel): fp32 buffers for up to
+// MQ_FUSED_MAX_N positions, in the decoder workspace (mq_fused_workspace_bytes).
+#define MQ_FUSED_MAX_N 64
+struct MqFusedArgs {
+  float* h;                    // [MQ_FUSED_MAX_N][H] residual stream
+  float* qkv;                  // [MQ_FUSED_MAX_N][4096] raw q | k | v projections
+  float* att;                  // [MQ_FUSED_MAX_N][2048] attention output
+  float* m;                    // [MQ_FUSED_MAX_N][I] silu(gate) * up
+  uint32_t* bar;               // grid-barrier counter stripes (32 x 128 bytes), zeroed per launch
+  const int32_t* tokens;       // device token ids [n]
+  int n;
+  const bf16_t* patch;         // optional bf16 rows replacing the embeddings [patch_start, +len)
+  int patch_start;
+  int patch_len;
+  int* tok_out;                // greedy next token
+  float* logits;               // optional fp32 [vocab] of the last position
+};
+size_t mq_fused_workspace_bytes();
+void mq_fused_bind(MqFusedArgs* f, char* base);
+// One cooperative launch over `grid` (>= 256) workgroups; 1 <= f.n <= MQ_FUSED_MAX_N.
+int mq_launch_prefill_fused(const MqDecodeParams& p, const MqFusedArgs& f, int grid,
+                            hipStream_t stream);
 // Whether a persistent launch starting at `pos` should use the long-context variant: every
 // workgroup of a group then holds an attention chunk in every step of the launch (positions
 // only grow within a launch), and the short-context local mode no longer applies.

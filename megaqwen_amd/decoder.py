@@ -508,10 +508,63 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
 
 class MegakernelFusedPrefillDecoder(MegakernelPrefillDecoder):
     """The reference's short-prompt decoder class (bindings_fused_prefill.cpp:286-545; default
-    max_prefill_len 64, `max_prefill_len()` a method) on the same HIP prefill and decode."""
+    max_prefill_len 64, `max_prefill_len()` a method).  Prompts of up to 64 tokens run the fused
+    prefill (`mq_prefill_fused`: one cooperative launch with the prefill megakernel's fp32
+    arithmetic, fused_prefill_megakernel_core.inl:658-745); a longer prompt, possible only with
+    max_prefill_len > 64, runs the multi-kernel bf16 prefill of MegakernelPrefillDecoder."""
+
+    FUSED_MAX = 64
 
     def __init__(self, embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight,
                  cos_table, sin_table, num_layers, max_seq_len, max_prefill_len=64, **kwargs):
         super().__init__(embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight,
                          cos_table, sin_table, num_layers, max_seq_len,
                          max_prefill_len=max_prefill_len, **kwargs)
+
+    def _fused(self, toks, emb=None, start: int = 0, return_logits: bool = False):
+        n = int(toks.numel())
+        if return_logits and self._logits is None:
+            self._logits = torch.empty(self.vocab_size, dtype=torch.float32, device=self._tok.device)
+        d = toks.to(device=self._tok.device, dtype=torch.int32).contiguous()
+        lg = self._logits.data_ptr() if return_logits else None
+        _lib.check(self._lib.mq_prefill_fused(
+            self._h, d.data_ptr(), n, emb.data_ptr() if emb is not None else None, start,
+            int(emb.shape[0]) if emb is not None else 0, self._tok.data_ptr() + 4, lg,
+            _stream_ptr()))
+        tok = int(self._tok[1].item())
+        return (tok, self._logits.clone()) if return_logits else tok
+
+    def prefill_step(self, input_token_ids) -> int:
+        """bindings_fused_prefill.cpp:235-283 (errors as :236-243)."""
+        toks = torch.as_tensor(input_token_ids).reshape(-1)
+        n = int(toks.numel())
+        if n == 0 or n > min(self.FUSED_MAX, int(self.max_prefill_len)):
+            return super().prefill_step(input_token_ids)
+        if int(toks.min()) < 0 or int(toks.max()) >= self.vocab_size:
+            raise ValueError("token id outside the vocabulary")
+        return self._fused(toks)
+
+    def prefill_step_with_logits(self, input_token_ids):
+        toks = torch.as_tensor(input_token_ids).reshape(-1)
+        n = int(toks.numel())
+        if n == 0 or n > min(self.FUSED_MAX, int(self.max_prefill_len)):
+            return super().prefill_step_with_logits(input_token_ids)
+        return self._fused(toks, return_logits=True)
+
+    def prefill_asr(self, input_token_ids, audio_embeds, audio_start_idx: int, *,
+                    return_logits: bool = False):
+        """bindings_fused_prefill.cpp:286-330; argument checks as the multi-kernel prefill_asr."""
+        toks = torch.as_tensor(input_token_ids).reshape(-1)
+        n = int(toks.numel())
+        if (n == 0 or n > min(self.FUSED_MAX, int(self.max_prefill_len))
+                or not isinstance(audio_embeds, torch.Tensor) or not audio_embeds.is_cuda
+                or audio_embeds.dtype != torch.bfloat16 or audio_embeds.dim() != 2
+                or int(audio_embeds.shape[1]) != 1024 or int(audio_embeds.shape[0]) <= 0
+                or int(audio_start_idx) < 0
+                or int(audio_start_idx) + int(audio_embeds.shape[0]) > n):
+            # the multi-kernel path raises the reference's errors for bad arguments
+            return super().prefill_asr(input_token_ids, audio_embeds, audio_start_idx,
+                                       return_logits=return_logits)
+        if int(toks.min()) < 0 or int(toks.max()) >= self.vocab_size:
+            raise ValueError("token id outside the vocabulary")
+        return self._fused(toks, audio_embeds.contiguous(), int(audio_start_idx), return_logits)

@@ -199,11 +199,14 @@ class OracleModel:
         tok = int(torch.argmax(logits).item())
         return (tok, logits) if return_logits else tok
 
-    def prefill_layer(self, li: int, h: torch.Tensor) -> torch.Tensor:
+    def prefill_layer(self, li: int, h: torch.Tensor, fused: bool = False) -> torch.Tensor:
         """Prefill layer li on the residual stream h [n, H] (bf16 values) at positions 0..n-1
         (fused_prefill_launch.inl:245-657): writes K/V rows 0..n-1 of layer li and returns the
-        layer output [n, H].  Every GEMM output and elementwise result is rounded to bf16."""
-        R = self._r
+        layer output [n, H].  Every GEMM output and elementwise result is rounded to bf16.
+        With `fused`, the prefill megakernel's arithmetic instead
+        (fused_prefill_megakernel_core.inl:35-599): fp32 throughout, attention over the fp32
+        normalised keys and values, and only the K/V cache rows rounded to bf16 (:313-315)."""
+        R = (lambda x: x) if fused else self._r
         w = self.layers[li]
         n = int(h.shape[0])
         c, s = self.cos[:n].unsqueeze(1), self.sin[:n].unsqueeze(1)
@@ -215,8 +218,8 @@ class OracleModel:
         v = R(nrm @ w["v"].T).view(n, self.nkv, self.D)
         q = R(rope(rms_norm(q, w["q_norm"]), c, s))
         k = R(rope(rms_norm(k, w["k_norm"]), c, s))
-        self.k_cache[li, :, :n] = k.transpose(0, 1)
-        self.v_cache[li, :, :n] = v.transpose(0, 1)
+        self.k_cache[li, :, :n] = bf16(k.transpose(0, 1)) if fused else k.transpose(0, 1)
+        self.v_cache[li, :, :n] = bf16(v.transpose(0, 1)) if fused else v.transpose(0, 1)
         qh = q.transpose(0, 1)                                          # [nq, n, D]
         kh = k.transpose(0, 1).repeat_interleave(self.group, dim=0)     # [nq, n, D]
         vh = v.transpose(0, 1).repeat_interleave(self.group, dim=0)
@@ -233,6 +236,33 @@ class OracleModel:
         m = R(silu(g) * u)
         d = R(m @ w["down"].T)
         return R(d + resid)
+
+    def prefill_fused(self, tokens, return_logits: bool = True, embeds=None,
+                      embeds_start: int = 0):
+        """The reference's prefill megakernel (prefill_megakernel,
+        fused_prefill_megakernel_core.inl:658-745, MegakernelFusedPrefillDecoder.prefill_step /
+        prefill_asr, bindings_fused_prefill.cpp:235-330): fp32 activations from the bf16
+        embedding rows (:3-33, audio rows :693-703), prefill_layer(fused=True) per layer, then
+        the fp32 final RMSNorm of the last position (:601-650) and the LM head.  Writes the
+        bf16 K/V rows 0..n-1 and sets position = n."""
+        toks = torch.as_tensor(tokens, dtype=torch.long).reshape(-1)
+        n = int(toks.numel())
+        if n == 0:
+            raise RuntimeError("Empty input sequence")
+        if n > self.max_seq_len:
+            raise RuntimeError("Prefill sequence length exceeds maximum")
+        h = self.embed[toks].clone()
+        if embeds is not None:
+            e = torch.as_tensor(embeds).to(self.dtype).reshape(-1, h.shape[1])
+            if e.shape[0] <= 0 or embeds_start < 0 or embeds_start + e.shape[0] > n:
+                raise RuntimeError("Invalid audio_start_idx/audio_len for the given seq_len")
+            h[embeds_start:embeds_start + e.shape[0]] = e
+        for li in range(self.L):
+            h = self.prefill_layer(li, h, fused=True)
+        logits = self.lm_head @ rms_norm(h[-1], self.final_norm)
+        self.position = n
+        tok = int(torch.argmax(logits).item())
+        return (tok, logits) if return_logits else tok
 
     def prefill_hidden_all(self, tokens):
         """fp32 logits for EVERY prompt position (no mutation of position semantics beyond

@@ -27,18 +27,20 @@ def to_cuda(weights: dict) -> dict:
 
 
 def build_pair(num_layers: int, vocab: int, max_seq: int, seed: int = 0, norm_jitter: float = 0.0,
-               max_prefill: int = 0, oracle: bool = True):
-    """(GPU decoder, CPU oracle or None, spec, cpu weights) on identical bf16 weights and tables."""
+               max_prefill: int = 0, oracle: bool = True, cls=None):
+    """(GPU decoder, CPU oracle or None, spec, cpu weights) on identical bf16 weights and tables.
+    `cls`: the decoder class (MegakernelPrefillDecoder by default)."""
     from megaqwen_amd.decoder import MegakernelPrefillDecoder
     from oracle.ref_cpu import OracleModel
+
+    cls = cls or MegakernelPrefillDecoder
 
     sp = spec(num_layers, vocab)
     w = make_weights(sp, seed=seed, norm_jitter=norm_jitter)
     cos, sin = build_rope_tables(max_seq, 1e6, 128)
     g = to_cuda(w)
-    dec = MegakernelPrefillDecoder(g["embed_weight"], g["layer_weights"], g["final_norm_weight"],
-                                   g["lm_head_weight"], cos.cuda(), sin.cuda(), num_layers,
-                                   max_seq, max_prefill_len=max_prefill)
+    dec = cls(g["embed_weight"], g["layer_weights"], g["final_norm_weight"], g["lm_head_weight"],
+              cos.cuda(), sin.cuda(), num_layers, max_seq, max_prefill_len=max_prefill)
     orc = OracleModel(w, sp, cos, sin, max_seq, round_bf16=True) if oracle else None
     return dec, orc, sp, w
 

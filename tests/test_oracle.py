@@ -176,6 +176,36 @@ def test_prefill_and_decode_agree_to_bf16_noise():
     assert m.position == 10
 
 
+def test_prefill_fused_is_the_pure_fp32_prefill_with_bf16_cache_rows():
+    """The prefill megakernel's arithmetic (prefill_fused) is the pure-fp32 model, which the
+    HuggingFace fixtures pin (round_bf16=False, test_golden_hf_prefill_and_decode): identical
+    logits, and cache rows that are exactly the bf16 rounding of that model's fp32 K/V rows.
+    It ignores the model's own rounding mode (the megakernel has no rounding points); a mistake
+    in the fused branch (a rounding left in, the cache rows unrounded) fails here."""
+    f, spec = _tiny_model(round_bf16=False)
+    r, _ = _tiny_model(round_bf16=True)
+    toks = make_tokens(13, spec["vocab_size"], seed=8)
+    _, lf = f.prefill(toks)
+    kf, vf = f.k_cache.clone(), f.v_cache.clone()
+    for m in (f, r):
+        m.reset()
+        _, lg = m.prefill_fused(toks)
+        assert torch.equal(lg, lf)
+        assert torch.equal(m.k_cache[:, :, :13], bf16(kf[:, :, :13]))
+        assert torch.equal(m.v_cache[:, :, :13], bf16(vf[:, :, :13]))
+        assert not torch.equal(m.k_cache[:, :, :13], kf[:, :, :13])
+        assert m.position == 13
+    # the embedding patch acts as in prefill
+    audio = bf16(torch.randn(3, 1024, generator=torch.Generator().manual_seed(5)))
+    f.reset()
+    _, lp = f.prefill(toks, embeds=audio, embeds_start=4)
+    f.reset()
+    _, lq = f.prefill_fused(toks, embeds=audio, embeds_start=4)
+    assert torch.equal(lp, lq)
+    with pytest.raises(RuntimeError):
+        f.prefill_fused([])
+
+
 def test_prefill_errors_and_position():
     m, spec = _tiny_model(layers=1)
     with pytest.raises(RuntimeError):
