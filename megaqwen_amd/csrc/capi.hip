@@ -107,7 +107,7 @@ struct mq_decoder {
   int grid;
   int pos;
   int max_prefill;
-  int early_kv_mode;       // -1: long-context variant chosen by position; 0 never; 1 always
+  int early_kv_mode;       // -1: long-context variant chosen by position; 0 never (default); 1 always
   size_t kv_bytes;
   char* ws;
   MqPrefillBuffers pf;
@@ -213,7 +213,10 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   p.attn_local_max = env_int("MEGAQWEN_ATTN_LOCAL_MAX", MQ_ATT_LOCAL_DEFAULT, 0, 1 << 20);
   p.early_kv = 0;
   p.nsteps = 1;
-  dec->early_kv_mode = env_int("MEGAQWEN_EARLY_KV", -1, -1, 1);
+  // the long-context variant (K rows issued a phase early) lost to the plain one once the
+  // exchanges carried tagged words: 646 against 659 us per token at pos 4096, 570 against 580
+  // at 1024 (A/B on one box), so it runs only when asked for
+  dec->early_kv_mode = env_int("MEGAQWEN_EARLY_KV", 0, -1, 1);
   dec->lay = lay;
   dec->mode = mode;
   dec->grid = grid;

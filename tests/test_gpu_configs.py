@@ -3,7 +3,7 @@
 - config 3: 16-token prompt, greedy decode from position 16 to 256 (local attention up to 176
   cached positions, the default MEGAQWEN_ATTN_LOCAL_MAX; split-K attention with the group merge
   above);
-- config 5: 4096-token prefill, then decode at 4096+ on the long-context kernel variant;
+- config 5: 4096-token prefill, then decode at 4096+ (every workgroup holds an attention chunk);
 - config 4: 512-token prefill, checked layer by layer through the per-layer trace hook;
 - chained decode (decode_steps_cuda / decode_greedy_cuda, up to 64 tokens per launch) against the
   oracle teacher-forced on the chain's tokens, and bit for bit against one launch per token;
@@ -148,9 +148,10 @@ def full4k():
 
 
 def test_config5_long_context_layerwise(full4k):
-    """4096 random tokens prefilled on the GPU, then decode at 4096.. on the
-    long-context kernel variant (every workgroup holds an attention chunk; K rows issued one
-    phase early).  The oracle takes over the GPU's KV cache; steps are checked layer by layer."""
+    """4096 random tokens prefilled on the GPU, then decode at 4096.. (every
+    workgroup holds an attention chunk; the kernel variant that issues K rows one phase early is
+    checked bit for bit against this default one in test_decode_early_kv_variant).  The oracle
+    takes over the GPU's KV cache; steps are checked layer by layer."""
     dec, orc, sp, _ = full4k
     dec.set_mode("persistent")
     dec.reset()
@@ -164,8 +165,8 @@ def test_config5_long_context_layerwise(full4k):
 
 
 def test_config5_chained_long_context_bitwise(full4k):
-    """The long-context variant chained (70 tokens: one 64-token launch and one of 6) against one
-    launch per token from the same 4096-token prefill: tokens and KV rows bit for bit."""
+    """Decode at 4096.. chained (70 tokens: one 64-token launch and one of 6) against one launch
+    per token from the same 4096-token prefill: tokens and KV rows bit for bit."""
     dec, _, sp, _ = full4k
     prompt = make_tokens(4096, VOCAB, seed=2)
     dec.set_mode("persistent")

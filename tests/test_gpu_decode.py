@@ -83,7 +83,7 @@ def test_decode_early_kv_variant(monkeypatch):
     """The long-context kernel variant (K rows issued with the q|k|v weights) is correct at any
     position: forced from the first step it matches the oracle, and it equals the other variant
     bit for bit wherever both use the same chunk layout (chunks above 8 positions), also after a
-    1000-token prefill, where the position-based choice picks it."""
+    1000-token prefill, where the position-based choice (MEGAQWEN_EARLY_KV=-1) picks it."""
     decs = {}
     for mode in ("1", "0"):
         monkeypatch.setenv("MEGAQWEN_EARLY_KV", mode)
