@@ -1478,10 +1478,9 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     __syncthreads();
   }
   const int h = wg % MQ_GROUPS, j = wg / MQ_GROUPS, NG = G / MQ_GROUPS;
-  // the sync wave's instructions (exchange polls, loads and stores) win issue arbitration
-  // over the compute waves' weight prefetches: 576.7 against 579.5 us per token at pos 128 (A/B
-  // on one box, repeated; unchanged at pos 4096)
-  if (wave_id() == MQ_SYNC_WAVE) __builtin_amdgcn_s_setprio(3);
+  // All waves keep the default issue priority.  Raising the sync wave's (s_setprio 3) helped
+  // while it alone polled counter barriers (576.7 against 579.5 us per token at pos 128); with
+  // every thread polling tagged words it costs 0.5% at pos 4096 (647.5 against 643.7 us).
   MqSync* sy = &p.st->sync;
   MqExchange* x = p.x;
   const int copy = wg % MQ_GROUPS;        // the exchange copy this workgroup reads
