@@ -74,6 +74,8 @@ def test_rejects_bad_shapes_and_args(lib):
     assert out.value is None
     assert lib.mq_decode_step(None, None, None, None, None) == _lib.MQ_ERR_INVALID_ARG
     assert lib.mq_prefill(None, None, 0, None, None, None) == _lib.MQ_ERR_INVALID_ARG
+    assert lib.mq_prefill_fused(None, None, 4, None, 0, 0, None, None, None) == \
+        _lib.MQ_ERR_INVALID_ARG
     assert lib.mq_decoder_position(None) == -1
     with pytest.raises(_lib.MegaQwenError):
         _lib.check(lib.mq_decoder_reset(None, None))
