@@ -143,3 +143,23 @@ def test_fused_class_long_prompt_runs_multikernel_prefill():
     err = float((lg.cpu() - olg).abs().max())
     assert err <= T.PREFILL_2L, err
     dec.check()
+
+
+def test_fused_prefill_then_both_decode_modes(small):
+    """The fused prefill leaves the decoder ready for either decode mode: after the same fused
+    prefill, 5 steps of the one-kernel-per-phase mode equal the persistent kernel's bit for bit."""
+    dec, _, _, _ = small
+    toks = make_tokens(30, dec.vocab_size, seed=21)
+    runs = []
+    for mode in ("persistent", "multi_kernel"):
+        dec.set_mode(mode)
+        dec.reset()
+        t = dec.prefill_step(toks)
+        lgs = []
+        for _ in range(5):
+            t, lg = dec.decode_step_with_logits(t)
+            lgs.append(lg)
+        runs.append(torch.stack(lgs))
+        dec.check()
+    dec.set_mode("persistent")
+    assert torch.equal(runs[0], runs[1])
