@@ -173,9 +173,23 @@ template <int BM, int BN, int MB, int NBK>
 MQ_DEV void qk_head_epilogue(const GemmArgs& g, const mq_f32x16 (&acc)[MB][NBK],
                              unsigned char* smem, int m_base, int n_base, int row0, int col0) {
   constexpr int TS = BN + 8;
+  constexpr int NR = BM / 16;                       // positions per thread group of 16
   bf16_t* T = reinterpret_cast<bf16_t*>(smem);
   static_assert(TS <= 2 * (GEMM_BK + 8), "the tile fits the A staging buffers (2 x BM rows)");
   const int t = threadIdx.x, lane = t & 63;
+  const int i = t & 15, d0 = 4 * i;
+  // the RoPE table entries of every position this thread handles, issued before the tile goes
+  // through LDS (inside the position loop each position waited for its own: 4096-token prefill
+  // 9.19 against 9.31 ms)
+  uint2 cl[NR], ch[NR], sl[NR], sh[NR];
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    const int pos = min(m_base + (t >> 4) + 16 * k, g.M - 1);
+    cl[k] = *reinterpret_cast<const uint2*>(g.cs + (size_t)pos * MQ_D + d0);
+    ch[k] = *reinterpret_cast<const uint2*>(g.cs + (size_t)pos * MQ_D + 64 + d0);
+    sl[k] = *reinterpret_cast<const uint2*>(g.sn + (size_t)pos * MQ_D + d0);
+    sh[k] = *reinterpret_cast<const uint2*>(g.sn + (size_t)pos * MQ_D + 64 + d0);
+  }
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -188,21 +202,17 @@ MQ_DEV void qk_head_epilogue(const GemmArgs& g, const mq_f32x16 (&acc)[MB][NBK],
   __syncthreads();
   const bool is_q = n_base < g.n0;
   const int h = (is_q ? n_base : n_base - g.n0) >> 7;
-  const int i = t & 15, d0 = 4 * i;
   const bf16_t* nw = is_q ? g.qn : g.kn;
   const uint2 nl = *reinterpret_cast<const uint2*>(nw + d0);
   const uint2 nh = *reinterpret_cast<const uint2*>(nw + 64 + d0);
   const float nwl[4] = {bf16_lo(nl.x), bf16_hi(nl.x), bf16_lo(nl.y), bf16_hi(nl.y)};
   const float nwh[4] = {bf16_lo(nh.x), bf16_hi(nh.x), bf16_lo(nh.y), bf16_hi(nh.y)};
-  for (int r = t >> 4; r < BM; r += 16) {
-    const int pos = m_base + r;
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    const int r = (t >> 4) + 16 * k, pos = m_base + r;
     if (pos >= g.M) break;     // whole 16-lane groups leave together
     const uint2 xl = *reinterpret_cast<const uint2*>(T + r * TS + d0);
     const uint2 xh = *reinterpret_cast<const uint2*>(T + r * TS + 64 + d0);
-    const uint2 cl = *reinterpret_cast<const uint2*>(g.cs + (size_t)pos * MQ_D + d0);
-    const uint2 ch = *reinterpret_cast<const uint2*>(g.cs + (size_t)pos * MQ_D + 64 + d0);
-    const uint2 sl = *reinterpret_cast<const uint2*>(g.sn + (size_t)pos * MQ_D + d0);
-    const uint2 sh = *reinterpret_cast<const uint2*>(g.sn + (size_t)pos * MQ_D + 64 + d0);
     const float lo[4] = {bf16_lo(xl.x), bf16_hi(xl.x), bf16_lo(xl.y), bf16_hi(xl.y)};
     const float hi[4] = {bf16_lo(xh.x), bf16_hi(xh.x), bf16_lo(xh.y), bf16_hi(xh.y)};
     float ss = 0.f;
@@ -210,10 +220,10 @@ MQ_DEV void qk_head_epilogue(const GemmArgs& g, const mq_f32x16 (&acc)[MB][NBK],
     for (int e = 0; e < 4; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
     ss = row16_sum(ss);
     const float rs = rsqrtf(ss * (1.0f / MQ_D) + MQ_EPS);
-    const float cosl[4] = {bf16_lo(cl.x), bf16_hi(cl.x), bf16_lo(cl.y), bf16_hi(cl.y)};
-    const float cosh_[4] = {bf16_lo(ch.x), bf16_hi(ch.x), bf16_lo(ch.y), bf16_hi(ch.y)};
-    const float sinl[4] = {bf16_lo(sl.x), bf16_hi(sl.x), bf16_lo(sl.y), bf16_hi(sl.y)};
-    const float sinh_[4] = {bf16_lo(sh.x), bf16_hi(sh.x), bf16_lo(sh.y), bf16_hi(sh.y)};
+    const float cosl[4] = {bf16_lo(cl[k].x), bf16_hi(cl[k].x), bf16_lo(cl[k].y), bf16_hi(cl[k].y)};
+    const float cosh_[4] = {bf16_lo(ch[k].x), bf16_hi(ch[k].x), bf16_lo(ch[k].y), bf16_hi(ch[k].y)};
+    const float sinl[4] = {bf16_lo(sl[k].x), bf16_hi(sl[k].x), bf16_lo(sl[k].y), bf16_hi(sl[k].y)};
+    const float sinh_[4] = {bf16_lo(sh[k].x), bf16_hi(sh[k].x), bf16_lo(sh[k].y), bf16_hi(sh[k].y)};
     bf16_t olo[4], ohi[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
