@@ -19,13 +19,9 @@ MQ_DEV float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 MQ_DEV float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 MQ_DEV float bf16_to_f32(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-// Round-to-nearest-even fp32 -> bf16 (the rounding torch and __float2bfloat16 use).
-MQ_DEV bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)0x7fc0;  // NaN stays NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
-}
+// Round-to-nearest-even fp32 -> bf16 (the rounding torch and __float2bfloat16 use): gfx950's
+// v_cvt_pk_bf16_f32 under the default rounding mode (a NaN stays a NaN).
+MQ_DEV bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 MQ_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
 // ---------------------------------------------------------------------------- loads

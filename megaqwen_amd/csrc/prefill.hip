@@ -29,8 +29,12 @@ typedef float mq_f32x16 __attribute__((ext_vector_type(16)));
 
 MQ_DEV mq_bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(mq_bf16x8, v); }
 MQ_DEV float silu_f(float x) { return x / (1.0f + expf(-x)); }
+typedef float mq_pf_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 mq_pf_bf16x2 __attribute__((ext_vector_type(2)));
+// Two values rounded to bf16 (nearest even) by one v_cvt_pk_bf16_f32; a in the low half.
 MQ_DEV uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+  const mq_pf_f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, mq_pf_bf16x2));
 }
 
 // ------------------------------------------------------------ attention operand layouts
