@@ -77,6 +77,16 @@ MQ_DEV void row_range(int n, int wg, int G, int& r0, int& nr) {
 // `load` issues the first PF items of every compute wave into registers (in the persistent
 // kernel, before the barrier that precedes the phase); `compute` finishes them against the fp32
 // vector in LDS and streams any further items (only for grids smaller than 256 workgroups).
+//
+// Paced prefetch (`paced`, the persistent kernel's prefetches): a wave sleeps MQ_PF_PACE x 64
+// clocks between its items.  The CU returns loads
+// in order, so an exchange's poll issued behind a burst of tens of KB of weight loads waits for
+// them to drain; issued a few KB at a time the weights still land within the exchange (which
+// lasts ~2.5 us) while the queue ahead of each poll stays short.  Measured per token, chained,
+// A/B on one box: pause 0 / 1 / 3 / 8 / 12 / 16 / 24 / 32 (x 64 clocks) gave 520.3 / 520.1 /
+// 520.7 / 518.9 / 516.7 / 518.1 / 534.7 / 556.7 us at pos 128 and 631.6 / 631.7 / 629.9 / 628.4 /
+// 628.0 / 631.0 / 650.3 / 675.0 us at pos 4096.
+#define MQ_PF_PACE 8
 template <int K, int S, int PF>
 struct RowSet {
   static constexpr int KS = K / S;
@@ -85,13 +95,14 @@ struct RowSet {
   uint4 w[PF][NL];
 
   template <class RowPtr>
-  MQ_DEV void load(RowPtr rowptr, int nr) {
+  MQ_DEV void load(RowPtr rowptr, int nr, bool paced = false) {
     const int lane = lane_id(), wave = wave_id();
     if (wave >= MQ_CWAVES) return;
     const int nitems = nr * S;
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       const int it = wave + j * MQ_CWAVES;
+      if (paced && j > 0) __builtin_amdgcn_s_sleep(MQ_PF_PACE);
       if (it < nitems) {
         const bf16_t* r = rowptr(it / S) + (it % S) * KS + lane * 8;
 #pragma unroll
@@ -893,12 +904,13 @@ MQ_DEV void o_publish(float* a_out, int wg, int G, const float* lds, float& res)
 }
 
 // ------------------------------------------------------------------------- P4: gate / up
-MQ_DEV void gu_load(GateUpSet& ws, const MqLayerW& w, int wg, int G) {
+MQ_DEV void gu_load(GateUpSet& ws, const MqLayerW& w, int wg, int G,
+                    bool paced = false) {
   int r0, nr;
   row_range(MQ_I, wg, G, r0, nr);
   ws.load([&](int i) {
     return i < nr ? w.wg + (size_t)(r0 + i) * MQ_H : w.wu + (size_t)(r0 + i - nr) * MQ_H;
-  }, 2 * nr);
+  }, 2 * nr, paced);
 }
 // Input: a in LDS_IN; gate and up dot products -> LDS_PR.
 MQ_DEV void gu_run(const GateUpSet& ws, const MqLayerW& w, int wg, int G, float* lds) {
@@ -942,10 +954,11 @@ MQ_DEV void hid_rows(int wg, int G, int& r0, int& nr) {
   r0 = 2 * p0;
   nr = 2 * np;
 }
-MQ_DEV void down_load(DownSet& ws, const MqLayerW& w, int wg, int G) {
+MQ_DEV void down_load(DownSet& ws, const MqLayerW& w, int wg, int G,
+                      bool paced = false) {
   int r0, nr;
   hid_rows(wg, G, r0, nr);
-  ws.load([&](int i) { return w.wd + (size_t)(r0 + i) * MQ_I; }, nr);
+  ws.load([&](int i) { return w.wd + (size_t)(r0 + i) * MQ_I; }, nr, paced);
 }
 // Input: m in LDS_IN; segment dot products -> LDS_PR.
 MQ_DEV void down_run(const DownSet& ws, const MqLayerW& w, int wg, int G, float* lds) {
@@ -1087,10 +1100,11 @@ MQ_DEV int grp_row(int h, int i) {
   if (i < 3 * MQ_D) return MQ_QDIM + h * MQ_D + (i - 2 * MQ_D);
   return MQ_QDIM + MQ_KVDIM + h * MQ_D + (i - 3 * MQ_D);
 }
-MQ_DEV void gqkv_load(QkvSet& ws, const MqLayerW& w, int h, int j, int NG) {
+MQ_DEV void gqkv_load(QkvSet& ws, const MqLayerW& w, int h, int j, int NG,
+                      bool paced = false) {
   int r0, nr;
   row_range(4 * MQ_D, j, NG, r0, nr);
-  ws.load([&](int i) { return qkv_row(w, grp_row(h, r0 + i)); }, nr);
+  ws.load([&](int i) { return qkv_row(w, grp_row(h, r0 + i)); }, nr, paced);
 }
 MQ_DEV void gqkv_run(const QkvSet& ws, const MqLayerW& w, int h, int j, int NG, float* lds) {
   norm_1024(lds + LDS_IN, w.in_ln, lds + LDS_XN, lds + LDS_RED);
@@ -1198,17 +1212,21 @@ MQ_DEV void group_merge(const float* part, int h, int nch, float* lds, int tag, 
 
 // GEMV over rows of 256 elements (the O projection restricted to one kv head's two query
 // heads): one wave instruction covers a pair of rows, lanes 0-31 the first and 32-63 the second.
+// `paced`: the items are paced as RowSet's are (only where the loads overlap an exchange: at the
+// split-mode partial exchange 562.0 against 566.7 us per token at pos 1024 and 619.2 against 627.7
+// at 4096; issued with local attention's K/V rows 521.5 against 518.4 at pos 128).
 template <int PF>
 struct PairSet {
   uint4 w[PF];
   template <class RowPtr>
-  MQ_DEV void load(RowPtr rowptr, int nr) {
+  MQ_DEV void load(RowPtr rowptr, int nr, bool paced) {
     const int lane = lane_id(), wave = wave_id();
     if (wave >= MQ_CWAVES) return;
     const int np = (nr + 1) / 2;
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int it = wave + i * MQ_CWAVES, row = 2 * it + (lane >> 5);
+      if (paced && i > 0) __builtin_amdgcn_s_sleep(MQ_PF_PACE);
       w[i] = (it < np && row < nr) ? ld_nt16(rowptr(row) + (lane & 31) * 8)
                                    : make_uint4(0, 0, 0, 0);
     }
@@ -1244,10 +1262,11 @@ typedef PairSet<3> OPairSet;   // 32 rows (16 pairs) per workgroup at 256 workgr
 MQ_DEV const bf16_t* opart_row(const MqLayerW& w, int h, int r) {
   return w.wo + (size_t)r * MQ_QDIM + 2 * h * MQ_D;
 }
-MQ_DEV void opart_load(OPairSet& ws, const MqLayerW& w, int h, int j, int NG) {
+MQ_DEV void opart_load(OPairSet& ws, const MqLayerW& w, int h, int j, int NG,
+                       bool paced = false) {
   int r0, nr;
   row_range(MQ_H, j, NG, r0, nr);
-  ws.load([&](int i) { return opart_row(w, h, r0 + i); }, nr);
+  ws.load([&](int i) { return opart_row(w, h, r0 + i); }, nr, paced);
 }
 // Input: att of the group's query heads in LDS_ATTH; dot products -> LDS_PR.
 MQ_DEV void opart_run(const OPairSet& ws, const MqLayerW& w, int h, int j, int NG, float* lds) {
@@ -1498,7 +1517,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
   GateUpSet wgu;
   DownSet wd;
   KvBlock kv;
-  if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG);
+  if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG, true);
   for (int step = 0; step < p.nsteps; ++step) {
     int pos, tok;
     if (!step_inputs(p, step == 0 ? p.tok_in : p.tok_out + (step - 1), pos, tok)) return;
@@ -1538,14 +1557,14 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
               // a workgroup without a chunk (some cache lengths below ~990 leave the last one
               // idle) takes the gate|up weights here, as in the other variant
               if (!ga.active) {
-                gu_load(wgu, w, wg, G);
+                gu_load(wgu, w, wg, G, true);
               } else {
                 kv_load_v<true>(kv, kv_base(p.vc, p, l, h), kv0, kv1, pos, kv_dummy);
                 if (ga.local) opart_load(wo, w, h, j, NG);
               }
             } else {
               if (!ga.active) {
-                gu_load(wgu, w, wg, G);
+                gu_load(wgu, w, wg, G, true);
               } else {
                 kv_block_load<false>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), kv0,
                                      kv1, pos, kv_dummy);
@@ -1564,7 +1583,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       if (!ga.local) {
         // chunk partials -> merge: tagged words of the group's slots, polled by every thread
         phase_step([&] { gattn_publish(p, l, pos, h, j, ga, lds, x->part[par], e); },
-                   [&] { opart_load(wo, w, h, j, NG); }, MQ_NOTHING);
+                   [&] { opart_load(wo, w, h, j, NG, true); }, MQ_NOTHING);
         group_merge(x->part[par], h, ga.nch, lds, (int)xtag(e), sy);
       }
       stamp(p, wg, l, 4);
@@ -1576,14 +1595,14 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
                    // local mode: the new position's K/V row (ALDS_KN/VN are still intact)
                    if (ga.local && ga.has_pos) attn_cache_row(p, l, h, pos, lds);
                  },
-                 [&] { if (ga.active) gu_load(wgu, w, wg, G); }, MQ_NOTHING);
+                 [&] { if (ga.active) gu_load(wgu, w, wg, G, true); }, MQ_NOTHING);
       gu_input_all(&x->opart[par][copy][0][0], lds, (int)xtag(e), sy);
       stamp(p, wg, l, 6);
       gu_run(wgu, w, wg, G, lds);
       stamp(p, wg, l, 7);
       // silu(gate) * up -> down: tagged words in every group's copy, polled by every thread
       phase_step([&] { gu_publish(&x->m[par][0][0], wg, G, lds, e); },
-                 [&] { down_load(wd, w, wg, G); }, MQ_NOTHING);
+                 [&] { down_load(wd, w, wg, G, true); }, MQ_NOTHING);
       m_input_all(x->m[par][copy], lds + LDS_IN, (int)xtag(e), sy);
       stamp(p, wg, l, 8);
       down_run(wd, w, wg, G, lds);
@@ -1597,7 +1616,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
           },
           [&] {
             if (l + 1 < p.num_layers) {
-              gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG);
+              gqkv_load(wq, lds_layer(s_layers, l + 1), h, j, NG, true);
               if constexpr (EARLY) k_early(l + 1);
             }
           },
@@ -1610,7 +1629,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
                 xep0 + (uint32_t)((step + 1) * p.num_layers));
     if (more) {
       // the next step's first weights do not depend on its token: in flight during the wait
-      if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG);
+      if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG, true);
       step_wait(p, epoch0 + (uint32_t)step + 1);
     }
   }
