@@ -79,14 +79,15 @@ MQ_DEV void row_range(int n, int wg, int G, int& r0, int& nr) {
 // vector in LDS and streams any further items (only for grids smaller than 256 workgroups).
 //
 // Paced prefetch (`paced`, the persistent kernel's prefetches): a wave sleeps MQ_PF_PACE x 64
-// clocks between its items.  The CU returns loads
-// in order, so an exchange's poll issued behind a burst of tens of KB of weight loads waits for
-// them to drain; issued a few KB at a time the weights still land within the exchange (which
-// lasts ~2.5 us) while the queue ahead of each poll stays short.  Measured per token, chained,
-// A/B on one box: pause 0 / 1 / 3 / 8 / 12 / 16 / 24 / 32 (x 64 clocks) gave 520.3 / 520.1 /
-// 520.7 / 518.9 / 516.7 / 518.1 / 534.7 / 556.7 us at pos 128 and 631.6 / 631.7 / 629.9 / 628.4 /
-// 628.0 / 631.0 / 650.3 / 675.0 us at pos 4096.
-#define MQ_PF_PACE 8
+// clocks between consecutive 1 KB wave loads.  The CU returns loads in order, so an exchange's
+// poll issued behind a burst of tens of KB of weight loads waits for them to drain; issued 1 KB
+// at a time the weights still land within the exchange (which lasts ~2.5 us) while the queue
+// ahead of each poll stays short.  Measured per token, chained, A/B on one box:
+//   pause between loads 0 / 2 / 3 / 4 / 5 / 6: 521.1 / 517.6 / 514.6 / 512.7 / 514.2 / 518.0 us
+//   at pos 128, 621.5 / 624.1 / 622.3 / 621.1 / 622.2 / 626.6 at pos 4096;
+//   pause between items (rows of 2 or 3 loads) instead, 0 / 1 / 3 / 8 / 12 / 16 / 24 / 32:
+//   520.3 / 520.1 / 520.7 / 518.9 / 516.7 / 518.1 / 534.7 / 556.7 us at pos 128.
+#define MQ_PF_PACE 4
 template <int K, int S, int PF>
 struct RowSet {
   static constexpr int KS = K / S;
@@ -102,11 +103,13 @@ struct RowSet {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       const int it = wave + j * MQ_CWAVES;
-      if (paced && j > 0) __builtin_amdgcn_s_sleep(MQ_PF_PACE);
       if (it < nitems) {
         const bf16_t* r = rowptr(it / S) + (it % S) * KS + lane * 8;
 #pragma unroll
-        for (int l = 0; l < NL; ++l) w[j][l] = ld_nt16(r + l * 512);
+        for (int l = 0; l < NL; ++l) {
+          if (paced && (j > 0 || l > 0)) __builtin_amdgcn_s_sleep(MQ_PF_PACE);
+          w[j][l] = ld_nt16(r + l * 512);
+        }
       } else {
 #pragma unroll
         for (int l = 0; l < NL; ++l) w[j][l] = make_uint4(0, 0, 0, 0);
@@ -1212,9 +1215,11 @@ MQ_DEV void group_merge(const float* part, int h, int nch, float* lds, int tag, 
 
 // GEMV over rows of 256 elements (the O projection restricted to one kv head's two query
 // heads): one wave instruction covers a pair of rows, lanes 0-31 the first and 32-63 the second.
-// `paced`: the items are paced as RowSet's are (only where the loads overlap an exchange: at the
-// split-mode partial exchange 562.0 against 566.7 us per token at pos 1024 and 619.2 against 627.7
-// at 4096; issued with local attention's K/V rows 521.5 against 518.4 at pos 128).
+// `paced`: a wave sleeps MQ_PF_PAIR_PACE x 64 clocks between its items (one 1 KB load each), only
+// where the loads overlap an exchange: at the split-mode partial exchange 562.0 against 566.7 us
+// per token at pos 1024 and 619.2 against 627.7 at 4096; issued with local attention's K/V rows
+// 521.5 against 518.4 at pos 128.
+#define MQ_PF_PAIR_PACE 8
 template <int PF>
 struct PairSet {
   uint4 w[PF];
@@ -1226,7 +1231,7 @@ struct PairSet {
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int it = wave + i * MQ_CWAVES, row = 2 * it + (lane >> 5);
-      if (paced && i > 0) __builtin_amdgcn_s_sleep(MQ_PF_PACE);
+      if (paced && i > 0) __builtin_amdgcn_s_sleep(MQ_PF_PAIR_PACE);
       w[i] = (it < np && row < nr) ? ld_nt16(rowptr(row) + (lane & 31) * 8)
                                    : make_uint4(0, 0, 0, 0);
     }
