@@ -27,5 +27,7 @@
 #define MQ_PART_STRIDE 132              // floats per attention partial: m, l, pad, pad, o[128]
 #define MQ_ATT_BLOCK (32 * MQ_CWAVES)   // 224 positions scored per pass of a chunk (32 per wave)
 #define MQ_ATT_SLOT (4 * MQ_CWAVES)     // 28: the smallest split-K chunk (4 positions per wave)
-#define MQ_ATT_LOCAL_DEFAULT 176       // default attn_local_max (persistent decode)
+#define MQ_ATT_LOCAL_DEFAULT MQ_ATT_BLOCK   // default attn_local_max (persistent decode): local
+                                             // attention while one 224-position block holds
+                                             // the cache
 #define MQ_GROUPS MQ_NKV                // persistent decode: workgroup wg serves kv head wg % 8

@@ -1,6 +1,6 @@
 """The BASELINE configurations at their real 28-layer shape, checked against the CPU oracle.
 
-- config 3: 16-token prompt, greedy decode from position 16 to 256 (local attention up to 176
+- config 3: 16-token prompt, greedy decode from position 16 to 256 (local attention up to 224
   cached positions, the default MEGAQWEN_ATTN_LOCAL_MAX; split-K attention with the group merge
   above);
 - config 5: 4096-token prefill, then decode at 4096+ (every workgroup holds an attention chunk);
@@ -52,14 +52,14 @@ def full272():
 
 def test_config3_decode_16_to_256_layerwise(full272):
     """16-token random prompt prefilled, then greedy decode from position 16
-    to 255.  Cache lengths up to 176 use the local attention (every workgroup of a kv-head group
-    over all positions); from 177 on the split-K chunks and the group merge run.  Checked layer
+    to 255.  Cache lengths up to 224 use the local attention (every workgroup of a kv-head group
+    over all positions); from 225 on the split-K chunks and the group merge run.  Checked layer
     by layer at positions on both sides of the switch and across the range."""
     dec, orc, sp, _ = full272
     dec.set_mode("persistent")
     dec.reset()
     nxt = dec.prefill_step(make_tokens(16, VOCAB, seed=0))
-    check = {16, 17, 40, 63, 64, 100, 127, 128, 174, 175, 176, 177, 191, 200, 254, 255}
+    check = {16, 17, 40, 63, 64, 100, 127, 128, 175, 191, 200, 222, 223, 224, 225, 254, 255}
     t = nxt
     for pos in range(16, 256):
         if pos in check:

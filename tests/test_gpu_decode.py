@@ -64,7 +64,7 @@ def test_decode_modes_bitwise_identical_and_deterministic(small):
 def test_decode_attention_split_and_local(monkeypatch, local_max):
     """Short-context attention both ways: split into position chunks with a merge barrier even at
     the first positions (local_max 0), and computed over all positions by every workgroup of a
-    kv-head group up to position 40 (local_max 512; the default uses it up to 176 positions).
+    kv-head group up to position 40 (local_max 512; the default uses it up to 224 positions).
     Each against the oracle, and persistent == one-kernel-per-phase bit for bit."""
     monkeypatch.setenv("MEGAQWEN_ATTN_LOCAL_MAX", str(local_max))
     dec, orc, sp, _ = build_pair(2, 151936, 128, seed=2, norm_jitter=0.1)
