@@ -154,6 +154,27 @@ int mq_debug_decode_step_timing(mq_decoder* dec, const int32_t* d_token_in,
  * decode kernels skip their barrier waits, so results are not meaningful. */
 int mq_decoder_check(mq_decoder* dec, void* stream);
 
+/* Exchange epochs of the persistent decode kernel.  No counterpart in the reference, whose
+ * cooperative grid.sync() needs none; they exist for tests and for callers that audit long runs.
+ * The persistent kernel hands values between workgroups as words that carry the epoch of the
+ * layer that wrote them.  The decoder state holds a base xep in [0, mq_exchange_epoch_period());
+ * the k-th layer run after it (k = step * num_layers + layer) uses epoch
+ * mq_exchange_epoch(xep, k), which is never 0 and runs through [1, period] cyclically, and a
+ * decode step of either mode advances the base to mq_exchange_epoch_advance(xep, num_layers).
+ * mq_exchange_tag(e) is the 2-bit tag the tagged (4-byte) exchange words carry for epoch e; the
+ * period is a multiple of 3, so consecutive epochs keep distinct tags across the wrap.  These four
+ * are pure host arithmetic (the same functions the kernels evaluate) and need no GPU. */
+uint32_t mq_exchange_epoch(uint32_t xep, uint64_t k);
+uint32_t mq_exchange_epoch_advance(uint32_t xep, uint64_t layers);
+uint32_t mq_exchange_tag(uint32_t epoch);
+uint32_t mq_exchange_epoch_period(void);
+/* Debug hooks: set (in stream order; MQ_ERR_INVALID_ARG unless xep < period) or read
+ * (synchronising `stream`) the decoder's exchange-epoch base, e.g. to run decode across the
+ * wrap of the epoch count without decoding ~10^8 tokens first.  Creation and mq_decoder_reset
+ * set it to 0. */
+int mq_debug_set_exchange_epoch(mq_decoder* dec, uint32_t xep, void* stream);
+int mq_debug_get_exchange_epoch(mq_decoder* dec, uint32_t* xep_out, void* stream);
+
 /* prefill_step (bindings_prefill.cpp:731-833) over launch_prefill_float
  * (fused_prefill_launch.inl:71-731): runs tokens d_tokens[0..n) at positions 0..n-1, fills the
  * KV cache, writes the greedy next token to d_token_out (and the last position's fp32 logits to
@@ -212,8 +233,10 @@ int mq_op_attention(mq_decoder* dec, int layer, const float* d_q, int cache_len,
  *     mq_op_attention, but the split-K partials live in a static device array of the library
  *     (640 KiB on each GPU it runs on, held until the process ends) instead of the decoder's
  *     workspace, and the call allocates nothing.  Calls that overlap on one GPU share that array
- *     and race.  Rejects cache lengths whose partials would exceed it (more than 64 position
- *     chunks per kv head) with MQ_ERR_INVALID_ARG. */
+ *     and race.  The array's size does not depend on the input: the split is capped at 64
+ *     position chunks per kv head, and the array holds that many partials, so every cache
+ *     length mq_op_attention accepts fits; cache_len outside [1, max_seq_len] (and a bad layer)
+ *     is rejected with MQ_ERR_INVALID_ARG before anything runs. */
 int mq_op_attention_noalloc(mq_decoder* dec, int layer, const float* d_q, int cache_len,
                             float* d_out, void* stream);
 /* (c) x_out = bf16(W_down(silu(W_gate n) * W_up n) + a), n = RMSNorm(a) * post_ln

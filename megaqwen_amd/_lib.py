@@ -31,7 +31,8 @@ EXPORTED = (
     "mq_decoder_set_host_position", "mq_decoder_set_position", "mq_decoder_set_mode", "mq_decoder_get_mode", "mq_decoder_grid", "mq_decode_step",
     "mq_decode_steps", "mq_debug_decode_step_layers", "mq_debug_decode_step_timing", "mq_decoder_check", "mq_prefill", "mq_prefill_embeds", "mq_prefill_fused", "mq_debug_prefill_layers", "mq_debug_prefill_buffers", "mq_op_qkv_rope", "mq_op_attention", "mq_op_attention_noalloc",
     "mq_op_mlp", "mq_op_decode_layer", "mq_op_lm_head", "mq_flash_attn_workspace_bytes",
-    "mq_flash_attn_bhwd",
+    "mq_flash_attn_bhwd", "mq_exchange_epoch", "mq_exchange_epoch_advance", "mq_exchange_tag",
+    "mq_exchange_epoch_period", "mq_debug_set_exchange_epoch", "mq_debug_get_exchange_epoch",
 )
 
 
@@ -70,7 +71,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     if not os.path.exists(path):
         raise ImportError(f"{path} is missing: build it with `python -m megaqwen_amd.build`")
     lib = ctypes.CDLL(path)
-    P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    P, I, S, U32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_uint32
     sig = {
         "mq_abi_version": (I, []),
         "mq_last_error": (ctypes.c_char_p, []),
@@ -103,6 +104,12 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "mq_op_lm_head": (I, [P, P, P, P, P]),
         "mq_flash_attn_workspace_bytes": (S, [I, I, I, I]),
         "mq_flash_attn_bhwd": (I, [P, P, P, P, I, I, I, I, I, ctypes.c_float, P, S, P]),
+        "mq_exchange_epoch": (U32, [U32, ctypes.c_uint64]),
+        "mq_exchange_epoch_advance": (U32, [U32, ctypes.c_uint64]),
+        "mq_exchange_tag": (U32, [U32]),
+        "mq_exchange_epoch_period": (U32, []),
+        "mq_debug_set_exchange_epoch": (I, [P, U32, P]),
+        "mq_debug_get_exchange_epoch": (I, [P, ctypes.POINTER(U32), P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -380,6 +380,29 @@ int mq_decoder_check(mq_decoder* dec, void* stream) {
   return MQ_OK;
 }
 
+uint32_t mq_exchange_epoch(uint32_t xep, uint64_t k) { return mq_xep_epoch(xep % MQ_XEP_PERIOD, k); }
+uint32_t mq_exchange_epoch_advance(uint32_t xep, uint64_t layers) {
+  return mq_xep_advance(xep % MQ_XEP_PERIOD, layers);
+}
+uint32_t mq_exchange_tag(uint32_t epoch) { return mq_xtag(epoch); }
+uint32_t mq_exchange_epoch_period(void) { return MQ_XEP_PERIOD; }
+
+int mq_debug_set_exchange_epoch(mq_decoder* dec, uint32_t xep, void* stream) {
+  if (dec == nullptr) return fail(MQ_ERR_INVALID_ARG, "decoder is NULL");
+  if (xep >= MQ_XEP_PERIOD)
+    return fail(MQ_ERR_INVALID_ARG, "exchange epoch base %u outside [0, %u)", xep, MQ_XEP_PERIOD);
+  if (mq_launch_set_xep(dec->p.st, xep, static_cast<hipStream_t>(stream)) != 0)
+    return fail(MQ_ERR_HIP, "state update failed");
+  return MQ_OK;
+}
+
+int mq_debug_get_exchange_epoch(mq_decoder* dec, uint32_t* xep_out, void* stream) {
+  if (dec == nullptr || xep_out == nullptr) return fail(MQ_ERR_INVALID_ARG, "NULL argument");
+  if (mq_read_xep(dec->p.st, static_cast<hipStream_t>(stream), xep_out) != 0)
+    return fail(MQ_ERR_HIP, "exchange-epoch readback failed");
+  return MQ_OK;
+}
+
 int mq_prefill(mq_decoder* dec, const int32_t* d_tokens, int n, int32_t* d_token_out,
                float* d_logits, void* stream) {
   if (dec == nullptr || d_tokens == nullptr || d_token_out == nullptr)
@@ -508,10 +531,6 @@ int mq_op_attention_noalloc(mq_decoder* dec, int layer, const float* d_q, int ca
     return fail(MQ_ERR_INVALID_ARG, "NULL argument");
   if (layer < 0 || layer >= dec->p.num_layers || cache_len < 1 || cache_len > dec->p.max_seq)
     return fail(MQ_ERR_INVALID_ARG, "layer %d / cache_len %d out of range", layer, cache_len);
-  if (mq_attn_nchunks(cache_len, dec->grid) > MQ_MAX_CHUNKS)
-    return fail(MQ_ERR_INVALID_ARG,
-                "cache_len %d needs more split-K partials than the static scratch holds (%d "
-                "chunks per kv head)", cache_len, MQ_MAX_CHUNKS);
   int rc = mq_launch_op_attention_noalloc(dec->p, layer, d_q, cache_len, d_out, dec->grid,
                                           static_cast<hipStream_t>(stream));
   if (rc == -1 || rc == -2)

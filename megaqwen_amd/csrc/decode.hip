@@ -189,9 +189,10 @@ MQ_DEV void wave_copy_bf16_1024(float* dst, const bf16_t* src) {
 
 // Sync wave: polls P (value, epoch) words per lane (word idx(i) of `src` for lane's i < P) until
 // every one carries epoch e, then hands out(i, value).  Only words still carrying an old epoch are
-// loaded again.  e == 0 takes the words as they are (written by an earlier kernel of the
-// one-kernel-per-phase mode).  A set error flag (read on every 16th round) or the spin bound ends
-// the wait early; the step's results are then invalid and mq_decoder_check reports it.
+// loaded again.  e == 0 takes the words as they are: only the one-kernel-per-phase mode passes
+// it, for words written by an earlier kernel; the persistent kernel's epochs are never 0
+// (mq_xep_epoch).  A set error flag (read on every 16th round) or the spin bound ends the wait
+// early; the step's results are then invalid and mq_decoder_check reports it.
 template <int P, class Idx, class Out>
 MQ_DEV void x_poll(const uint64_t* src, Idx idx, uint32_t e, MqSync* sy, Out out) {
   const int lane = lane_id();
@@ -268,8 +269,9 @@ MQ_DEV void phase_finish(Epi epilogue) {
 // every layer needs every workgroup's values.  The one-kernel-per-phase mode publishes the same
 // truncated values with the same epochs (and reads without polling), so the modes stay
 // bit-identical and either may follow the other; the truncation is below 2^-22 relative, far
-// under the bf16 rounding these values meet downstream.
-MQ_DEV uint32_t xtag(uint32_t e) { return 1u + e % 3u; }
+// under the bf16 rounding these values meet downstream.  The epochs of consecutive layers stay
+// consecutive across the wrap of the epoch count (mq_xep_epoch), so the three tags stay distinct.
+MQ_DEV uint32_t xtag(uint32_t e) { return mq_xtag(e); }
 MQ_DEV uint32_t tag_bits(float v, uint32_t e) { return (__float_as_uint(v) & ~3u) | xtag(e); }
 MQ_DEV float untag(uint32_t u) { return __uint_as_float(u & ~3u); }
 MQ_DEV void st_tag(float* p, float v, uint32_t e) {
@@ -534,10 +536,21 @@ MQ_DEV void attn_cache_row(const MqDecodeParams& p, int layer, int h, int pos, c
 // The row of the position being decoded (pos_new) is never loaded: it is written during this
 // step (attn_cache_row) and enters the softmax from LDS instead (ALDS_SNEW / ALDS_VN).  Fetching
 // it before the write would leave a stale copy in this CU's L1 and this XCD's L2, and a chained
-// launch reads the row with plain loads in the next step.  Every row below pos_new was written by
-// an earlier step (of this launch, with device-scope stores ordered by the barriers in between,
-// or of an earlier kernel) and was not loaded by anyone before that write, so a plain load of it
-// cannot hit a stale line.
+// launch reads the row with plain loads in the next step.  Every row below pos_new was written
+// either by an earlier kernel (complete at the kernel boundary) or by an earlier step of this
+// launch, and was not loaded by anyone before that write, so a plain load of it cannot hit a
+// stale line.  Within a launch, what completes the row before any later step loads it:
+//   1. the sync wave stores the row with device-scope (sc1) stores in a phase_step epilogue
+//      (attn_cache_row: with the O partials in local mode, with the attention partial in split
+//      mode) and, in the same phase_step, waits for all its memory operations
+//      (wait_all_memory, s_waitcnt vmcnt(0), which counts stores) before the closing
+//      __syncthreads;
+//   2. so the store has completed before wave 0 of that workgroup, after that barrier, adds its
+//      arrival to the LM head's completion count (lm_head_run);
+//   3. the last arriver publishes the step-done epoch only after observing every arrival, and
+//      every workgroup issues the next step's K/V loads only after step_wait has seen that epoch.
+// No barrier between workgroups is involved: the exchanges within a step carry epoch- or
+// tag-stamped words and order nothing else.
 #define MQ_ATT_PER_WAVE (MQ_ATT_BLOCK / MQ_CWAVES)
 static_assert(MQ_ATT_PER_WAVE == 32, "two 16-position MFMA column groups per compute wave");
 struct KvBlock {
@@ -1058,7 +1071,7 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
         if (advance_pos)
           __hip_atomic_store(&p.st->pos.v, (uint32_t)(pos + 1), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
-        if (set_xep)   // any value, 0 included (the 32-bit epoch count wraps)
+        if (set_xep)   // the next base, already reduced (mq_xep_advance; 0 is a valid base)
           __hip_atomic_store(&p.st->xep.v, xep_next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(&sy->done.v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
@@ -1543,8 +1556,10 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     for (int l = 0; l < p.num_layers; ++l) {
       const MqLayerW w = lds_layer(s_layers, l);
       const int par = l & 1;
-      // exchange epoch of this step and layer (never 0, never reused: the base only grows)
-      const uint32_t e = xep0 + (uint32_t)(step * p.num_layers + l) + 1u;
+      // exchange epoch of this step and layer: never 0, and consecutive layers have consecutive
+      // epochs (cyclic in [1, MQ_XEP_PERIOD]), so a buffer's previous words carry other epochs
+      // and other tags
+      const uint32_t e = mq_xep_epoch(xep0, (uint64_t)step * (uint32_t)p.num_layers + (uint32_t)l);
       stamp(p, wg, l, 0);
       gqkv_run(wq, w, h, j, NG, lds);
       stamp(p, wg, l, 1);
@@ -1631,7 +1646,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     const bool more = step + 1 < p.nsteps;
     lm_head_run(p, wg, G, lds, p.tok_out + step, p.nsteps == 1 ? p.logits : nullptr, pos, true,
                 false, more, epoch0 + (uint32_t)step + 1, true,
-                xep0 + (uint32_t)((step + 1) * p.num_layers));
+                mq_xep_advance(xep0, (uint64_t)(step + 1) * (uint32_t)p.num_layers));
     if (more) {
       // the next step's first weights do not depend on its token: in flight during the wait
       if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG, true);
@@ -1657,12 +1672,12 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
   const bf16_t* xe = p.embed + (size_t)tok * MQ_H;
   // the (value, epoch) words of this mode carry epoch 0: written by a completed earlier kernel,
   // they are read without waiting (copy 0 of the grid-wide buffers).  Its tagged words carry the
-  // epoch the persistent kernel would give this layer (xep + l + 1; the LM-head kernel advances
-  // xep by num_layers), so a persistent launch after steps of this mode never finds a stale
-  // tagged word whose two tag bits match its expected epoch.
-  const uint32_t et = __builtin_amdgcn_readfirstlane(
-      __hip_atomic_load(&p.st->xep.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) +
-      (uint32_t)l + 1u;
+  // epoch the persistent kernel would give this layer (mq_xep_epoch(xep, l); the LM-head kernel
+  // advances xep by num_layers), so a persistent launch after steps of this mode never finds a
+  // stale tagged word whose two tag bits match its expected epoch.
+  const uint32_t xep = __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(&p.st->xep.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const uint32_t et = mq_xep_epoch(xep, (uint32_t)l);
   const uint64_t* xprev = x->h[(l + 1) & 1][0];   // layer l - 1's output
   // the layer input: the embedding row for layer 0, else the previous layer's output
   auto load_x = [&](float* dst) {
@@ -1674,9 +1689,9 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_phase_kernel(MqDecodePar
       if (p.num_layers == 0) wave_copy_bf16_1024(lds + LDS_IN, xe);
       else hidden_gather(lds + LDS_IN, nullptr, x->h[(p.num_layers - 1) & 1][0], 0, sy);
     });
-    // et - 1 = xep: the step's epochs were xep + 1 .. xep + num_layers
+    // the step's epochs were mq_xep_epoch(xep, 0 .. num_layers - 1)
     lm_head_run(p, wg, G, lds, p.tok_out, p.logits, pos, true, false, false, 0, true,
-                et - 1u + (uint32_t)p.num_layers);
+                mq_xep_advance(xep, (uint32_t)p.num_layers));
   } else {
     const MqLayerW w = p.layers[l];
     if constexpr (PH == 0) {
@@ -2277,6 +2292,10 @@ __global__ void mq_fill_state_kernel(MqState* st, int pos, int clear_err) {
     st->steps.v = 0;
   }
 }
+// Debug: the exchange-epoch base (validated by the caller: xep < MQ_XEP_PERIOD).
+__global__ void mq_set_xep_kernel(MqState* st, uint32_t xep) {
+  if (threadIdx.x == 0) st->xep.v = xep;
+}
 __global__ void mq_zero_kernel(uint4* p, size_t n16) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
        i += (size_t)gridDim.x * blockDim.x)
@@ -2408,6 +2427,20 @@ int mq_launch_zero(void* ptr, size_t bytes, hipStream_t stream) {
   return launch_status();
 }
 
+int mq_launch_set_xep(MqState* st, uint32_t xep, hipStream_t stream) {
+  if (xep >= MQ_XEP_PERIOD) return -3;
+  mq_set_xep_kernel<<<1, 64, 0, stream>>>(st, xep);
+  return launch_status();
+}
+
+int mq_read_xep(MqState* st, hipStream_t stream, uint32_t* xep_out) {
+  uint32_t v = 0;
+  if (hipMemcpyAsync(&v, &st->xep.v, 4, hipMemcpyDeviceToHost, stream) != hipSuccess) return -1;
+  if (hipStreamSynchronize(stream) != hipSuccess) return -1;
+  *xep_out = v;
+  return 0;
+}
+
 int mq_read_error(MqState* st, hipStream_t stream, uint32_t* err_out) {
   uint32_t v = 0;
   if (hipMemcpyAsync(&v, &st->sync.err.v, 4, hipMemcpyDeviceToHost, stream) != hipSuccess)
@@ -2441,6 +2474,12 @@ int mq_launch_op_attention(const MqDecodeParams& p, int layer, const float* q_ha
 // GPU's copy comes from hipGetSymbolAddress, resolved once per device with that device current.
 static __device__ __align__(256) unsigned char scratch[MQ_NOALLOC_SCRATCH_BYTES];
 static_assert(sizeof(MqScratch) <= MQ_NOALLOC_SCRATCH_BYTES, "scratch holds one MqScratch");
+// The split is capped at MQ_MAX_CHUNKS chunks per kv head (mq_attn_nchunks) and MqScratch.part
+// holds that many, so every cache length the entry point accepts ([1, max_seq_len]) fits: the
+// array's size does not depend on the input.
+static_assert(sizeof(MqScratch::part) ==
+                  sizeof(float) * MQ_NKV * MQ_MAX_CHUNKS * MQ_GQA * MQ_PART_STRIDE,
+              "one partial slot per chunk the split can produce");
 
 #define MQ_NOALLOC_MAX_DEVICES 64
 static std::mutex g_scratch_mu;
@@ -2463,7 +2502,6 @@ static int scratch_address(void** out) {
 
 int mq_launch_op_attention_noalloc(const MqDecodeParams& p, int layer, const float* q_hat,
                                    int cache_len, float* att_out, int grid, hipStream_t stream) {
-  if (mq_attn_nchunks(cache_len, grid) > MQ_MAX_CHUNKS) return -3;
   void* s = nullptr;
   const int rc = scratch_address(&s);
   if (rc != 0) return rc;

@@ -71,12 +71,31 @@ MQ_DEV uint64_t xword(float v, uint32_t e) { return ((uint64_t)e << 32) | __floa
 MQ_DEV float xvalue(uint64_t w) { return __uint_as_float((uint32_t)w); }
 MQ_DEV uint32_t xepoch(uint64_t w) { return (uint32_t)(w >> 32); }
 
+// Exchange epochs.  Layer k (k = step * num_layers + l, counted from the launch's first layer)
+// of a launch whose state holds base xep (0 <= xep < MQ_XEP_PERIOD) exchanges its values under
+// epoch 1 + (xep + k) mod MQ_XEP_PERIOD, and the launch leaves (xep + layers run) mod
+// MQ_XEP_PERIOD behind for the next one.  So an epoch is never 0 (the value the one-kernel-per-
+// phase mode writes into its epoch words, and a cleared buffer holds), and the epochs of
+// consecutive layers run 1, 2, ..., MQ_XEP_PERIOD, 1, 2, ... without a break: MQ_XEP_PERIOD is a
+// multiple of 3, so the tags 1 + e mod 3 of the tagged words also stay distinct for e, e - 1 and
+// e - 2 across the wrap.  (A 32-bit count that simply wrapped would give epoch 0 after 2^32
+// layers, about 153 M tokens at 28 layers, and two equal tags in a row there.)
+#define MQ_XEP_PERIOD 3221225472u      // 3 * 2^30
+__host__ __device__ inline uint32_t mq_xep_epoch(uint32_t xep, uint64_t k) {
+  return 1u + (uint32_t)(((uint64_t)xep + k) % MQ_XEP_PERIOD);
+}
+__host__ __device__ inline uint32_t mq_xep_advance(uint32_t xep, uint64_t layers) {
+  return (uint32_t)(((uint64_t)xep + layers) % MQ_XEP_PERIOD);
+}
+__host__ __device__ inline uint32_t mq_xtag(uint32_t e) { return 1u + e % 3u; }
+
 struct MqState {
   MqSync sync;
   MqLine pos;                  // device-side decode position (read at step start, +1 at step end)
   MqLine steps;                // completed steps of multi-step launches (the step-done epoch)
-  MqLine xep;                  // exchange epochs used so far (+num_layers per persistent step);
-                               // only creation and reset, which clear MqExchange, zero it
+  MqLine xep;                  // exchange-epoch base in [0, MQ_XEP_PERIOD): advanced by
+                               // mq_xep_advance(xep, num_layers) per decode step of either mode;
+                               // creation and reset, which clear MqExchange, zero it
 };
 
 struct MqDecodeParams {
@@ -183,6 +202,9 @@ int mq_launch_clear_state(MqState* st, MqExchange* x, hipStream_t stream);
 int mq_launch_zero(void* ptr, size_t bytes, hipStream_t stream);
 int mq_decode_grid(int mode, int* grid_out);
 int mq_read_error(MqState* st, hipStream_t stream, uint32_t* err_out);
+// Debug: sets / reads the exchange-epoch base MqState.xep (set: xep < MQ_XEP_PERIOD, else -3).
+int mq_launch_set_xep(MqState* st, uint32_t xep, hipStream_t stream);
+int mq_read_xep(MqState* st, hipStream_t stream, uint32_t* xep_out);
 
 // op-level launchers (per-op microbenchmarks and parity tests)
 int mq_launch_op_qkv_rope(const MqDecodeParams& p, int layer, const bf16_t* x, int pos,

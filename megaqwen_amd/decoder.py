@@ -198,6 +198,17 @@ class MegakernelDecoder:
         out[..., list(self._CYCLE_COLUMNS)] = d
         return out
 
+    def debug_set_exchange_epoch(self, xep: int) -> None:
+        """Sets the exchange-epoch base of the persistent kernel's cross-workgroup words (in
+        stream order), e.g. just below the wrap of the epoch count; results do not depend on it."""
+        _lib.check(self._lib.mq_debug_set_exchange_epoch(self._h, int(xep), _stream_ptr()))
+
+    def debug_exchange_epoch(self) -> int:
+        """The current exchange-epoch base (synchronises the stream)."""
+        v = ctypes.c_uint32()
+        _lib.check(self._lib.mq_debug_get_exchange_epoch(self._h, ctypes.byref(v), _stream_ptr()))
+        return int(v.value)
+
     def set_position(self, position: int) -> None:
         """Moves the decode position (host and device) without touching the KV cache; the
         chat.py binding passes the position with every call (chat.py:448-470)."""
@@ -475,11 +486,23 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
     def _advance_host_position(self, n: int) -> None:
         self._set_host_position(self.position() + int(n))
 
-    def decode_greedy_cuda(self, first_token_id: int, max_new_tokens: int, eos_ids, chunk: int = 32):
-        """GPU-resident greedy loop with a chunked EOS scan (bindings_prefill.cpp:1159-1349).
-        Returns (tokens int32[k] on the device, k, stop_code) where tokens[0] is the first
-        token and tokens[i] the token fed to step i; generation stops before the first EOS
-        (stop_code 1) or after max_new_tokens steps (stop_code 0)."""
+    def decode_greedy_cuda(self, first_token_id: int, max_new_tokens: int, eos_ids, chunk: int = 32,
+                           *, scan_chunk_tail: bool = False):
+        """GPU-resident greedy loop with a chunked EOS scan (bindings_prefill.cpp:1159-1349,
+        its default coop backend).  Returns (tokens int32[k] on the device, k, stop_code) where
+        tokens[0] is the first token and tokens[i] the token fed to step i.
+
+        Each chunk of `steps` decode steps feeds toks[0] (the previous chunk's last output, or
+        the first token) and produces toks[1..steps]; toks[0..steps-1] are appended to the
+        result.  As in the reference, only toks[1..steps-1] are scanned for an EOS id (none when
+        steps == 1): the chunk's tail token toks[steps] becomes the next chunk's toks[0], which
+        is emitted but never scanned, so an EOS produced as a chunk's last step does not stop
+        generation, and on the final chunk the tail is not emitted at all.  On the first scanned
+        EOS the result ends just before it (stop_code 1); otherwise after max_new_tokens entries
+        (stop_code 0).  The position advances by every decoded step, as in the reference.
+
+        scan_chunk_tail=True (not in the reference) also scans toks[steps], so the result is
+        exactly the greedy sequence up to, not including, its first EOS after the first token."""
         max_new = int(max_new_tokens)
         if max_new <= 0:
             return torch.empty(0, dtype=torch.int32, device=self._tok.device), 0, 0
@@ -496,9 +519,10 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
             steps = min(chunk, max_new - gen)
             toks = self._chain(nxt, steps)
             out[gen:gen + steps] = toks[:steps]
-            hit = torch.isin(toks[1:steps + 1], eos).nonzero()
+            end = steps + 1 if scan_chunk_tail else steps     # scanned: toks[1:end]
+            hit = torch.isin(toks[1:end], eos).nonzero() if end > 1 else None
             gen += steps
-            if hit.numel() > 0:
+            if hit is not None and hit.numel() > 0:
                 first = int(hit[0, 0]) + 1          # index in toks of the EOS token
                 kept = gen - steps + first
                 return out[:kept], kept, 1

@@ -5,9 +5,12 @@
 - `MegakernelPrefillGenerator(model_name, max_seq_len, max_prefill_len)` runs the prompt through
   the MFMA prefill, then decodes (:67-128). It adds `prefill_only(prompt) -> (next_token,
   position)`.
-- `MegakernelFusedPrefillGenerator` keeps the reference's name for its small-prompt fused
-  prefill generator (default `max_prefill_len=64`). Here it runs the same MFMA prefill, since
-  that one path serves every prompt length.
+- `MegakernelFusedPrefillGenerator` is the reference's small-prompt generator (default
+  `max_prefill_len=64`, megakernel_generators.py:131-190). Its decoder,
+  `MegakernelFusedPrefillDecoder`, runs prompts of up to 64 tokens through the fused prefill
+  (`mq_prefill_fused`: one cooperative launch with the reference prefill megakernel's fp32
+  activations) and longer ones, when max_prefill_len allows them, through the multi-kernel MFMA
+  prefill.
 
 Generation stops at a stop token (the tokenizer's EOS by default), after `max_new_tokens`, or
 when the position reaches `max_seq_len - 1`, as the reference's loops do. `temperature` is
@@ -114,8 +117,8 @@ class MegakernelPrefillGenerator:
 
 
 class MegakernelFusedPrefillGenerator(MegakernelPrefillGenerator):
-    """Name and defaults of the reference's small-prompt generator
-    (megakernel_generators.py:131-190); runs the MFMA prefill."""
+    """The reference's small-prompt generator (megakernel_generators.py:131-190): prompts of up
+    to 64 tokens run the fused prefill (`mq_prefill_fused`) of MegakernelFusedPrefillDecoder."""
 
     _decoder_cls = MegakernelFusedPrefillDecoder
 

@@ -105,3 +105,40 @@ def test_decode_kernels_do_not_spill():
         assert u.get("ScratchSize", -1) == 0, (name, u)
     for name in persistent:
         assert usage[name]["VGPRs"] + usage[name].get("AGPRs", 0) <= 256, usage[name]
+
+
+def test_exchange_epoch_arithmetic(lib):
+    """The persistent decode kernel hands values between workgroups as words carrying the epoch
+    of the layer that wrote them (64-bit words) or a 2-bit tag of it (4-byte words); a reader
+    must never take a stale word for a fresh one.  Checked here on the library's own epoch
+    functions (the ones the kernels evaluate) at bases around the wrap of the epoch count:
+    an epoch is never 0 (0 means "take the word without waiting" and is what cleared buffers and
+    the one-kernel-per-phase mode hold), consecutive layers get cyclically consecutive epochs,
+    the tags of any three consecutive epochs differ (a buffer alternates by layer parity, so the
+    word a reader may still see was written one or two epochs earlier), and the base a launch
+    leaves behind continues the sequence exactly."""
+    P = lib.mq_exchange_epoch_period()
+    assert P % 3 == 0 and P >= 1 << 31
+    L, steps = 28, 64                    # layers per step, steps per chained launch
+    bases = [0, 1, 2, 12345, P // 2, P - 3, P - 2, P - 1, P - L * steps, P - L * steps - 1]
+    for b in bases:
+        prev = []
+        for k in range(2 * L * steps):
+            e = lib.mq_exchange_epoch(b, k)
+            assert 1 <= e <= P, (b, k, e)
+            if prev:
+                assert e == prev[-1] % P + 1, (b, k, e, prev[-1])
+            window = [e] + prev[-2:]
+            tags = [lib.mq_exchange_tag(x) for x in window]
+            assert all(1 <= t <= 3 for t in tags) and len(set(tags)) == len(tags), (b, k, window)
+            prev.append(e)
+    for b in bases:
+        for n in (0, 1, L, L * steps, P - 1, P, 2 * P + 5, (1 << 40) + 7):
+            nb = lib.mq_exchange_epoch_advance(b, n)
+            assert 0 <= nb < P
+            for k in (0, 1, 2 * L):
+                assert lib.mq_exchange_epoch(nb, k) == lib.mq_exchange_epoch(b, n + k), (b, n, k)
+    # far past one period (a decoder never reset for years): still never 0
+    for k in (P - 1, P, 2 * P - 1, 1 << 33, (1 << 40) + 3):
+        for b in (0, P - 1):
+            assert lib.mq_exchange_epoch(b, k) != 0

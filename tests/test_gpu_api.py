@@ -83,7 +83,11 @@ def test_op_decode_layer_matches_oracle_and_decoder(pair):
 
 
 def test_chat_decode_ldg_matches_decoder(pair):
-    dec, _, sp, w = pair
+    """chat.py's decode_ldg / decode_ldg_with_logits over caller-owned caches: against the CPU
+    oracle directly (teacher-forced, north-star 2e-2 on the logits, greedy tokens wherever the
+    oracle's top-2 margin exceeds twice the error) and against the decoder bit for bit."""
+    from tests import tolerances as T
+    dec, orc, sp, w = pair
     g = to_cuda(w)
     L, S = sp["num_layers"], 256
     cos, sin = build_rope_tables(S, 1e6, 128)
@@ -96,12 +100,18 @@ def test_chat_decode_ldg_matches_decoder(pair):
     vc = torch.zeros_like(kc)
     scratch = [torch.zeros(16, device="cuda") for _ in range(11)]
     dec.reset()
+    orc.reset()
     toks = make_tokens(8, sp["vocab_size"], seed=21).tolist()
     for pos, t in enumerate(toks):
         args = (t, g["final_norm_weight"], g["lm_head_weight"], cos, sin, kc, vc, *scratch,
                 L, pos, pos + 1, S)
+        otok, olg = orc.decode_step(t)
         if pos % 2:
             got, lg = k.decode_ldg_with_logits(*args)
+            err = float((lg.cpu() - olg).abs().max())
+            assert err <= T.DECODE_LOGITS, (pos, err)
+            if top2_margin(olg) > 2 * err + 1e-6:
+                assert got == otok, pos
             ref, rlg = dec.decode_step_with_logits(t)
             assert torch.equal(lg, rlg), pos
         else:

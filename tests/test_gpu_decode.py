@@ -344,19 +344,86 @@ def test_mode_switches_without_reset(small):
     dec.check()
 
 
-def test_decode_greedy_cuda_eos(small):
+def test_exchange_epoch_wrap(small):
+    """Decoding across the wrap of the exchange-epoch count.  The epoch base is set just below
+    the wrap (debug hook) so that a chained persistent launch crosses it inside one launch, at a
+    layer in the middle of a step; tokens and every KV-cache row must equal the one-kernel-per-
+    phase mode from a fresh state bit for bit (the epochs change no value), the base left behind
+    must continue the epoch sequence, and steps of both modes may alternate across the wrap."""
     dec, _, sp, _ = small
+    lib = dec._lib
+    P, L = lib.mq_exchange_epoch_period(), sp["num_layers"]
+    first = int(make_tokens(1, sp["vocab_size"], seed=31)[0])
+    n = 40
+    dec.set_mode("multi_kernel")
+    dec.reset()
+    assert dec.debug_exchange_epoch() == 0
+    ref = dec.decode_steps_cuda(first, n).cpu().tolist()
+    kref, vref = dec.k_cache[:, :, :n].clone(), dec.v_cache[:, :, :n].clone()
+    for base in (P - (n // 2) * L + 1, P - 1):
+        dec.set_mode("persistent")
+        dec.reset()
+        dec.debug_set_exchange_epoch(base)
+        chain = dec.decode_steps_cuda(first, n).cpu().tolist()
+        assert chain == ref, base
+        assert torch.equal(dec.k_cache[:, :, :n], kref) and torch.equal(dec.v_cache[:, :, :n], vref)
+        assert dec.debug_exchange_epoch() == lib.mq_exchange_epoch_advance(base, n * L)
+        dec.check()
+    # alternating modes across the wrap, one step each
+    dec.reset()
+    dec.debug_set_exchange_epoch(P - 3 * L - 1)
+    t = first
+    for i in range(8):
+        dec.set_mode("multi_kernel" if i % 2 else "persistent")
+        t = dec.decode_step(t)
+        assert t == ref[i], i
+    dec.set_mode("persistent")
+    assert dec.decode_steps_cuda(t, 6).cpu().tolist() == ref[8:14]
+    with pytest.raises(RuntimeError):
+        dec.debug_set_exchange_epoch(P)
+    dec.check()
+
+
+def test_decode_greedy_cuda_eos(small):
+    """decode_greedy_cuda against the reference's loop (bindings_prefill.cpp:1296-1340, restated
+    in oracle/greedy_ref.py) over the GPU's own greedy sequence: an EOS inside a chunk, an EOS
+    produced as a chunk's last step (emitted, decoding goes on), an EOS produced as the final
+    chunk's last step (not emitted, stop code 0), chunks of one step (never scanned), and no EOS
+    at all; tokens, count, stop code and the position advance.  With scan_chunk_tail=True the
+    result is the greedy prefix before the first EOS."""
+    from oracle.greedy_ref import decode_greedy_reference as ref
+    dec, _, sp, _ = small
+    dec.set_mode("persistent")
     first = int(make_tokens(1, sp["vocab_size"], seed=7)[0])
     dec.reset()
-    seq = [first] + dec.decode_steps_cuda(first, 40).cpu().tolist()
-    eos = seq[17]
-    stop_at = seq.index(eos, 1)
-    dec.reset()
-    out, k, code = dec.decode_greedy_cuda(first, 40, [eos], chunk=8)
-    assert code == 1 and k == stop_at and out.cpu().tolist() == seq[:stop_at]
-    dec.reset()
-    out, k, code = dec.decode_greedy_cuda(first, 30, [-5], chunk=7)
-    assert code == 0 and k == 30 and out.cpu().tolist() == seq[:30]
+    seq = [first] + dec.decode_steps_cuda(first, 48).cpu().tolist()
+
+    def fresh(j):          # seq[j] does not occur earlier among the decoded tokens
+        return seq[j] not in seq[1:j]
+
+    cases = [(40, 8, seq[17]), (30, 7, -5), (12, 1, seq[5])]
+    tail = [j for j in range(8, 40, 8) if fresh(j)]
+    assert tail, f"no fresh token at a chunk tail of {seq}"
+    cases.append((40, 8, seq[tail[0]]))                         # a chunk's last step
+    final = [m for m in range(20, 47) if fresh(m) and m % 6 != 0]
+    assert final, f"no fresh token for a final-chunk tail in {seq}"
+    cases.append((final[0], 6, seq[final[0]]))                  # the final chunk's last step
+    exercised = 0
+    for max_new, chunk, eos in cases:
+        want = ref(seq, max_new, [eos], chunk, with_steps=True)
+        dec.reset()
+        out, k, code = dec.decode_greedy_cuda(first, max_new, [eos], chunk=chunk)
+        assert (out.cpu().tolist(), k, code) == want[:3], (max_new, chunk, eos)
+        assert dec.position() == want[3], (max_new, chunk, eos)
+        dec.reset()
+        out2, k2, code2 = dec.decode_greedy_cuda(first, max_new, [eos], chunk=chunk,
+                                                 scan_chunk_tail=True)
+        js = [j for j in range(1, max_new + 1) if seq[j] == eos]
+        assert (out2.cpu().tolist(), k2, code2) == ((seq[:js[0]], js[0], 1) if js
+                                                   else (seq[:max_new], max_new, 0))
+        exercised += (k, code) != (k2, code2)
+    assert exercised >= 2     # the tail cases differ between the two scans
+    dec.check()
 
 
 def test_reset_and_position_semantics(small):

@@ -5,10 +5,12 @@ bf16; fused_prefill_megakernel_core.inl:658-745).
 
 The GPU forms every product exactly (fp32 activations split into three bf16 parts on MFMA) and
 differs from the oracle only in the order of fp32 sums and in applying the RMSNorm scale after
-the dot product, so the logits are held to the north-star 2e-2 and the measured error is printed
-(it is far below).  K/V cache rows are bf16 roundings of fp32 values that agree to ~1e-6, so a
-few round the other way: within one bf16 ulp (K: plus the head's ulp, RoPE can cancel) and
->= 98% bit-equal.
+the dot product, so the prefill logits are held to T.FUSED_PREFILL (2e-5; measured 2.6e-6 ..
+4.4e-6), which a bf16 activation anywhere, or the split without its lo part, would exceed
+(tests/test_oracle_spread.py plants both in the oracle).  Decode steps that follow the prefill
+run the decode kernel and are held to the north-star 2e-2.  K/V cache rows are bf16 roundings
+of fp32 values that agree to ~1e-6, so a few round the other way: within one bf16 ulp (K: plus
+the head's ulp, RoPE can cancel) and >= 98% bit-equal.
 """
 import ctypes
 
@@ -50,7 +52,7 @@ def _check_prefill(dec, orc, n, seed, **kw):
         assert _close_bf16(kc[li, :, :n], orc.k_cache[li, :, :n], head_ulp=True), f"k layer {li}"
     err = float((lg.cpu() - olg).abs().max())
     print(f"fused prefill n={n}: logit error {err:.3e} (max |logit| {float(olg.abs().max()):.2f})")
-    assert err <= T.DECODE_LOGITS, err
+    assert err <= T.FUSED_PREFILL, err
     if top2_margin(olg) > 2 * err + 1e-6:
         assert tok == otok
     dec.check()

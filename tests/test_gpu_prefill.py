@@ -72,6 +72,27 @@ def test_prefill_matches_oracle(small, n):
     dec.check()
 
 
+@pytest.mark.parametrize("n", [7, 64, 512])
+def test_prefill_vs_unrounded_fp32_model(small, n):
+    """The GPU prefill against the unrounded fp32 oracle (the HF-pinned model, no bf16 rounding
+    points): the distance is the reference's bf16 rounding (PREFILL_ROUNDING_2L on the CPU
+    oracle) plus the GPU's own summation order, within T.PREFILL_VS_FP32_2L, with the same
+    greedy token wherever the pinned model's top-2 margin exceeds twice the error."""
+    from oracle.ref_cpu import OracleModel
+    dec, orc, sp, w = small
+    pinned = OracleModel(w, sp, orc.cos, orc.sin, orc.max_seq_len, round_bf16=False)
+    toks = make_tokens(n, sp["vocab_size"], seed=n)
+    dec.reset()
+    tok, lg = dec.prefill_step_with_logits(toks)
+    otok, olg = pinned.prefill(toks)
+    err = float((lg.cpu() - olg).abs().max())
+    print(f"prefill n={n} vs the unrounded fp32 model: logit error {err:.3e}")
+    assert err <= T.PREFILL_VS_FP32_2L, err
+    if top2_margin(olg) > 2 * err + 1e-6:
+        assert tok == otok
+    dec.check()
+
+
 def test_decode_after_prefill(small):
     dec, orc, sp, _ = small
     toks = make_tokens(37, sp["vocab_size"], seed=11)

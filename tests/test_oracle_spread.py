@@ -83,6 +83,67 @@ def test_unrounded_oracle_within_north_star_at_2_layers():
     assert worst < T.DECODE_LOGITS
 
 
+def test_prefill_rounding_points_vs_unrounded_model_2_layers():
+    """The multi-kernel prefill's bf16 rounding points (fused_prefill_launch.inl:245-657) against
+    the unrounded fp32 model that the HF fixtures pin (tests/test_oracle.py), on the 2-layer
+    prefill cases of test_gpu_prefill.py.  The rounded oracle must stay within bf16 noise of the
+    pinned model (PREFILL_ROUNDING_2L) with the same argmax, and must differ from it by at least
+    PREFILL_ROUNDING_2L_MIN: a rounding point lost from the oracle (and so possibly from the
+    kernel it checks) shrinks the distance.  The unrounded fp32 model's own fp32-vs-fp64 spread
+    is ~4e-6 here, so the distance is the rounding's alone."""
+    sp = spec(2, VOCAB)
+    w = make_weights(sp, seed=2, norm_jitter=0.1)
+    cos, sin = build_rope_tables(640, 1e6, 128)
+    mr = OracleModel(w, sp, cos, sin, 640, round_bf16=True)
+    mp = OracleModel(w, sp, cos, sin, 640, round_bf16=False)
+    mp64 = OracleModel(w, sp, cos, sin, 640, round_bf16=False, dtype=torch.float64)
+    worst = 0.0
+    for n in (1, 7, 64, 100, 512):
+        toks = make_tokens(n, VOCAB, seed=n)
+        a, b, c = mr.prefill(toks)[1], mp.prefill(toks)[1], mp64.prefill(toks)[1]
+        d = float((a - b).abs().max())
+        print(f"prefill n={n}: rounded vs unrounded {d:.3e}, unrounded fp32 vs fp64 "
+              f"{float((b.double() - c).abs().max()):.1e}")
+        assert float((b.double() - c).abs().max()) < 1e-4
+        assert int(a.argmax()) == int(b.argmax()), n
+        worst = max(worst, d)
+    assert T.PREFILL_ROUNDING_2L_MIN <= worst <= T.PREFILL_ROUNDING_2L, worst
+
+
+def test_fused_prefill_bound_separates_reduced_precision():
+    """FUSED_PREFILL (the fused prefill's logit bound against its fp32 oracle) is tight enough
+    to fail a fused prefill that lost precision: planted in the CPU oracle, activations kept to
+    16 significant bits at the RMSNorm outputs (the GPU's three-part bf16 split of an fp32
+    activation without its lo part) or rounded to bf16 there move the logits beyond it."""
+    import oracle.ref_cpu as R
+    sp = spec(2, VOCAB)
+    w = make_weights(sp, seed=5, norm_jitter=0.1)
+    cos, sin = build_rope_tables(64, 1e6, 128)
+    m = OracleModel(w, sp, cos, sin, 64)
+    orig = R.rms_norm
+
+    def keep16(x):                      # 16 significant bits: the hi and mid parts only
+        mant, ex = torch.frexp(x)
+        return torch.ldexp(torch.round(mant * 2 ** 16) / 2 ** 16, ex)
+
+    try:
+        for n in (1, 16):
+            toks = make_tokens(n, VOCAB, seed=100 + n)
+            m.reset()
+            ref = m.prefill_fused(toks)[1]
+            R.rms_norm = lambda x, w_, eps=R.EPS: keep16(orig(x, w_, eps))
+            m.reset()
+            d16 = float((m.prefill_fused(toks)[1] - ref).abs().max())
+            R.rms_norm = lambda x, w_, eps=R.EPS: R.bf16(orig(x, w_, eps))
+            m.reset()
+            d8 = float((m.prefill_fused(toks)[1] - ref).abs().max())
+            R.rms_norm = orig
+            print(f"n={n}: lo part dropped {d16:.2e}, bf16 norms {d8:.2e}")
+            assert d16 > T.FUSED_PREFILL and d8 > 100 * T.FUSED_PREFILL, (n, d16, d8)
+    finally:
+        R.rms_norm = orig
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_dtype_mode_keeps_rounding_points(dtype):
     """The fp64 mode rounds where the fp32 mode does: the K/V cache rows and every layer output

@@ -25,6 +25,24 @@ PREFILL_2L = 4e-2
 PREFILL_28L_SPREAD = 3.66e-2
 PREFILL_28L = 7e-2
 
+# the multi-kernel prefill's bf16 rounding points (bf16 after every op, as launch_prefill_float)
+# against the unrounded fp32 model that the HF fixtures pin, on the CPU oracle (2 layers, seed 2,
+# norm jitter 0.1, n in {1, 7, 64, 100, 512}, tokens of seed n): 1.85e-2 .. 2.90e-2 (n = 64).
+# tests/test_oracle_spread.py holds the oracle between these two bounds: the rounding points
+# must move the logits (a lost rounding point shrinks the distance) but only by bf16 noise.
+PREFILL_ROUNDING_2L_MIN = 1.0e-2
+PREFILL_ROUNDING_2L = 3.0e-2
+# GPU multi-kernel prefill against the unrounded fp32 oracle, same 2-layer cases (n in {7, 64,
+# 512}): the rounding above plus the GPU's own fp32 summation order (PREFILL_2L_SPREAD)
+PREFILL_VS_FP32_2L = 5e-2
+
+# fused short-prompt prefill (tests/test_gpu_fused_prefill.py) against the oracle's restatement
+# of the prefill megakernel (fp32 activations, bf16 weights): measured 2.6e-6 .. 4.4e-6 at n in
+# {1, 7, 16, 20, 24, 33, 64} with 2 and 28 layers; held at 2e-5.  On the CPU oracle, activations
+# kept to 16 significant bits (the three-part bf16 split without its lo part) move the logits by
+# 3.4e-5 .. 6.5e-5, bf16 norm outputs by 8.7e-3 .. 1.7e-2 (tests/test_oracle_spread.py).
+FUSED_PREFILL = 2e-5
+
 # flash_attn_bhwd (tests/test_gpu_flash_attn.py): the output is the 16-bit rounding of an fp32
 # evaluation, so it must lie within half a unit in the last place of the float64 oracle plus the
 # fp32 evaluation's own error.  That error is bounded by the P hi + lo split (2^-18 of max|v| for
