@@ -376,7 +376,7 @@ int mq_decoder_check(mq_decoder* dec, void* stream) {
   uint32_t err = 0;
   if (mq_read_error(dec->p.st, static_cast<hipStream_t>(stream), &err) != 0)
     return fail(MQ_ERR_HIP, "error-flag readback failed");
-  if (err != 0) return fail(MQ_ERR_DEVICE, "device error flag %u (1 = barrier time-out, 2 = bad position/token)", err);
+  if (err != 0) return fail(MQ_ERR_DEVICE, "device error flag %u (1 = exchange time-out, 2 = bad position/token, 4 = workgroup placement)", err);
   return MQ_OK;
 }
 

@@ -278,6 +278,10 @@ MQ_DEV void st_tag(float* p, float v, uint32_t e) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), tag_bits(v, e), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
 }
+// The same for a word read only on the writer's XCD (st_local32).
+MQ_DEV void st_tag_local(float* p, float v, uint32_t e) {
+  st_local32(reinterpret_cast<uint32_t*>(p), tag_bits(v, e));
+}
 MQ_DEV bool tag_ok2(uint64_t w, uint32_t tag) {
   return ((uint32_t)w & 3u) == tag && ((uint32_t)(w >> 32) & 3u) == tag;
 }
@@ -1006,7 +1010,7 @@ MQ_DEV void down_publish(int wg, int G, const float* lds, float& res, Out out) {
 MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int* tok_out,
                         float* logits, int pos, bool advance_pos, bool round_norm = false,
                         bool publish_epoch = false, uint32_t step_epoch = 0,
-                        bool set_xep = false, uint32_t xep_next = 0) {
+                        bool set_xep = false, uint32_t xep_next = 0, bool reset_place = false) {
   float* xn = lds + LDS_XN;
   uint64_t* keys = reinterpret_cast<uint64_t*>(lds + LDS_KEYS);
   norm_1024(lds + LDS_IN, p.final_norm, xn, lds + LDS_RED, round_norm);
@@ -1073,6 +1077,9 @@ MQ_DEV void lm_head_run(const MqDecodeParams& p, int wg, int G, float* lds, int*
                              __HIP_MEMORY_SCOPE_AGENT);
         if (set_xep)   // the next base, already reduced (mq_xep_advance; 0 is a valid base)
           __hip_atomic_store(&p.st->xep.v, xep_next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (reset_place)   // a launch's last step: every workgroup claimed its role at its start
+          for (int i = 0; i < MQ_GROUPS; ++i)
+            __hip_atomic_store(&p.st->place[i].v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(&sy->done.v, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       if (publish_epoch) {
@@ -1131,11 +1138,17 @@ MQ_DEV void gqkv_run(const QkvSet& ws, const MqLayerW& w, int h, int j, int NG, 
              [&](int it, float v) { lds[LDS_PR + it] = v; });
 }
 // Sync-wave epilogue: this workgroup's rows of group h's q|k|v as (value, epoch e) words into
-// xq [4 * MQ_D] (the group's local row order, grp_row).
-MQ_DEV void gqkv_publish(uint64_t* xq, uint32_t e, int j, int NG, const float* lds) {
+// xq [4 * MQ_D] (the group's local row order, grp_row).  `local`: every reader is on this XCD
+// (the persistent kernel places a group on one XCD), so plain stores into its L2 suffice.
+MQ_DEV void gqkv_publish(uint64_t* xq, uint32_t e, int j, int NG, const float* lds,
+                         bool local = false) {
   int r0, nr;
   row_range(4 * MQ_D, j, NG, r0, nr);
-  for (int t = lane_id(); t < nr; t += 64) st_coh64(xq + r0 + t, xword(lds[LDS_PR + t], e));
+  for (int t = lane_id(); t < nr; t += 64) {
+    const uint64_t w = xword(lds[LDS_PR + t], e);
+    if (local) st_local64(xq + r0 + t, w);
+    else st_coh64(xq + r0 + t, w);
+  }
 }
 
 // Position chunks of a group: as many chunks of at least one register slot (28 positions) as
@@ -1203,17 +1216,22 @@ MQ_DEV void gattn_publish_local(const MqDecodeParams& p, int layer, int pos, int
 // empty partial (m = -inf, l = 0, o = 0; never read), so that every slot is rewritten in every
 // split-mode layer, as the tags require.
 MQ_DEV void gattn_publish(const MqDecodeParams& p, int layer, int pos, int h, int j,
-                          const GAttn& g, const float* lds, float* part, uint32_t e) {
+                          const GAttn& g, const float* lds, float* part, uint32_t e,
+                          bool local = false) {
   const int lane = lane_id();
+  auto put = [&](float* q, float v) {
+    if (local) st_tag_local(q, v, e);
+    else st_tag(q, v, e);
+  };
   if (j < MQ_GROUP_CHUNKS) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = lane + 64 * i, jj = t >> 7, d = t & 127;
-      st_tag(part_ptr(part, h, j, jj) + 4 + d, g.active ? lds[ALDS_ORED + t] : 0.f, e);
+      put(part_ptr(part, h, j, jj) + 4 + d, g.active ? lds[ALDS_ORED + t] : 0.f);
     }
     if (lane < 2) {
-      st_tag(part_ptr(part, h, j, lane), g.active ? lds[ALDS_STAT + lane] : -INFINITY, e);
-      st_tag(part_ptr(part, h, j, lane) + 1, g.active ? lds[ALDS_STAT + 2 + lane] : 0.f, e);
+      put(part_ptr(part, h, j, lane), g.active ? lds[ALDS_STAT + lane] : -INFINITY);
+      put(part_ptr(part, h, j, lane) + 1, g.active ? lds[ALDS_STAT + 2 + lane] : 0.f);
     }
   }
   if (g.has_pos) attn_cache_row(p, layer, h, pos, lds);
@@ -1377,6 +1395,21 @@ MQ_DEV void hidden_gather(float* dst, float* dst2, const uint64_t* src, uint32_t
     if (dst2 != nullptr) reinterpret_cast<float2*>(dst2)[lane + 64 * i] = f;
   });
 }
+// All threads: the same, thread t polling pair word t (one per thread), then __syncthreads.  Every
+// wave polls its own 64 words, so the exchange has 8 waves' loads in flight instead of the sync
+// wave's 8 per lane.
+MQ_DEV void hidden_input_all(float* dst, float* dst2, const uint64_t* src, uint32_t e,
+                             MqSync* sy) {
+  static_assert(MQ_H / 2 == MQ_THREADS, "one pair word per thread");
+  const int t = tid();
+  x_poll<1>(src, [&](int) { return t; }, e, sy, [&](int, float v) {
+    const uint32_t u = __float_as_uint(v);
+    const float2 f = make_float2(bf16_to_f32((bf16_t)(u & 0xffffu)), bf16_to_f32((bf16_t)(u >> 16)));
+    reinterpret_cast<float2*>(dst)[t] = f;
+    reinterpret_cast<float2*>(dst2)[t] = f;
+  });
+  __syncthreads();
+}
 MQ_DEV void input_hidden_bf16(float* lds, const bf16_t* src) {
   wave_copy_bf16_1024(lds + LDS_IN, src);
   wave_copy_bf16_1024(lds + LDS_HID, src);
@@ -1506,7 +1539,7 @@ template <bool EARLY>
 __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDecodeParams p) {
   __shared__ __align__(16) float lds[MQ_LDS_FLOATS];
   __shared__ MqLayerW s_layers[MQ_MAX_LAYERS];
-  const int G = gridDim.x, wg = blockIdx.x;
+  const int G = gridDim.x;
   {
     const int nw = p.num_layers * (int)(sizeof(MqLayerW) / 4);
     for (int i = tid(); i < nw; i += MQ_THREADS)
@@ -1514,15 +1547,38 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
     q_operand_clear(lds);
     __syncthreads();
   }
-  const int h = wg % MQ_GROUPS, j = wg / MQ_GROUPS, NG = G / MQ_GROUPS;
+  // Workgroup roles from the hardware placement: kv-head group h is the XCD the workgroup runs
+  // on, member j the order in which it claimed a slot there, so the group-local exchanges (plain
+  // stores into the XCD's L2, st_local64) are read only on their writer's XCD whatever the
+  // dispatch order.  The workgroup's role index rw = h + 8 j takes the place of its launch index
+  // in every row assignment (a bijection onto [0, G) when every XCD holds G / 8 workgroups, as
+  // one 512-thread workgroup per CU on 8 XCDs of G / 8 CUs gives).  Any other placement claims a
+  // member index >= G / 8 somewhere: that workgroup flags error 4 and returns, and the others'
+  // waits end on the error flag.  The claims are reset by the launch's last step.
+  __shared__ int s_role;
+  if (tid() == 0) {
+    const uint32_t xc = (uint32_t)xcc_id() & (MQ_GROUPS - 1);
+    const uint32_t c = __hip_atomic_fetch_add(&p.st->place[xc].v, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    s_role = (int)(xc + MQ_GROUPS * c);
+  }
+  __syncthreads();
+  const int NG = G / MQ_GROUPS;
+  const int rw = __builtin_amdgcn_readfirstlane(s_role);
+  const int h = rw % MQ_GROUPS, j = rw / MQ_GROUPS;
+  if (j >= NG) {
+    if (tid() == 0)
+      __hip_atomic_store(&p.st->sync.err.v, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   // All waves keep the default issue priority.  Raising the sync wave's (s_setprio 3) helped
   // while it alone polled counter barriers (576.7 against 579.5 us per token at pos 128); with
   // every thread polling tagged words it costs 0.5% at pos 4096 (647.5 against 643.7 us).
   MqSync* sy = &p.st->sync;
   MqExchange* x = p.x;
-  const int copy = wg % MQ_GROUPS;        // the exchange copy this workgroup reads
+  const int copy = h;                     // the exchange copy this workgroup reads (its XCD's)
   int r0h, nrh;
-  hid_rows(wg, G, r0h, nrh);
+  hid_rows(rw, G, r0h, nrh);
   // the step-done epoch and the exchange epoch base before this launch: read by every workgroup
   // before any can complete the first step (completion needs every workgroup's arrival at the
   // LM head, where the last one advances them)
@@ -1560,9 +1616,9 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       // epochs (cyclic in [1, MQ_XEP_PERIOD]), so a buffer's previous words carry other epochs
       // and other tags
       const uint32_t e = mq_xep_epoch(xep0, (uint64_t)step * (uint32_t)p.num_layers + (uint32_t)l);
-      stamp(p, wg, l, 0);
+      stamp(p, rw, l, 0);
       gqkv_run(wq, w, h, j, NG, lds);
-      stamp(p, wg, l, 1);
+      stamp(p, rw, l, 1);
       // q|k|v -> attention: epoch words inside the kv-head group.  The gate|up weights go out two
       // phases ahead, during the attention phase, from workgroups without an attention chunk;
       // the others issue them after the O projection (a deep queue stalls the issue of loads and
@@ -1571,20 +1627,20 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
       // the q|k|v dot products (whose loads are conditional), they made the compiler's wait for
       // the q|k|v weights wait for them too.
       phase_step(
-          [&] { gqkv_publish(x->q[par][h], e, j, NG, lds); },
+          [&] { gqkv_publish(x->q[par][h], e, j, NG, lds, true); },
           [&] {
             if constexpr (EARLY) {
               // a workgroup without a chunk (some cache lengths below ~990 leave the last one
               // idle) takes the gate|up weights here, as in the other variant
               if (!ga.active) {
-                gu_load(wgu, w, wg, G, true);
+                gu_load(wgu, w, rw, G, true);
               } else {
                 kv_load_v<true>(kv, kv_base(p.vc, p, l, h), kv0, kv1, pos, kv_dummy);
                 if (ga.local) opart_load(wo, w, h, j, NG);
               }
             } else {
               if (!ga.active) {
-                gu_load(wgu, w, wg, G, true);
+                gu_load(wgu, w, rw, G, true);
               } else {
                 kv_block_load<false>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), kv0,
                                      kv1, pos, kv_dummy);
@@ -1597,41 +1653,41 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
             if (ga.active)
               attn_input(x->q[par][h], e, sy, w.q_norm, w.k_norm, cs, sn, p.scale_log2, lds);
           });
-      stamp(p, wg, l, 2);
+      stamp(p, rw, l, 2);
       if (ga.active) attn_core(p, l, h, ga.p0, ga.p1, pos, ga.has_new, kv, lds, ga.local);
-      stamp(p, wg, l, 3);
+      stamp(p, rw, l, 3);
       if (!ga.local) {
         // chunk partials -> merge: tagged words of the group's slots, polled by every thread
-        phase_step([&] { gattn_publish(p, l, pos, h, j, ga, lds, x->part[par], e); },
+        phase_step([&] { gattn_publish(p, l, pos, h, j, ga, lds, x->part[par], e, true); },
                    [&] { opart_load(wo, w, h, j, NG, true); }, MQ_NOTHING);
         group_merge(x->part[par], h, ga.nch, lds, (int)xtag(e), sy);
       }
-      stamp(p, wg, l, 4);
+      stamp(p, rw, l, 4);
       opart_run(wo, w, h, j, NG, lds);
-      stamp(p, wg, l, 5);
+      stamp(p, rw, l, 5);
       // O partials -> a: tagged words in every group's copy, polled by every thread
       phase_step([&] {
                    opart_publish(&x->opart[par][0][0][0], h, j, NG, lds, e);
                    // local mode: the new position's K/V row (ALDS_KN/VN are still intact)
                    if (ga.local && ga.has_pos) attn_cache_row(p, l, h, pos, lds);
                  },
-                 [&] { if (ga.active) gu_load(wgu, w, wg, G, true); }, MQ_NOTHING);
+                 [&] { if (ga.active) gu_load(wgu, w, rw, G, true); }, MQ_NOTHING);
       gu_input_all(&x->opart[par][copy][0][0], lds, (int)xtag(e), sy);
-      stamp(p, wg, l, 6);
-      gu_run(wgu, w, wg, G, lds);
-      stamp(p, wg, l, 7);
+      stamp(p, rw, l, 6);
+      gu_run(wgu, w, rw, G, lds);
+      stamp(p, rw, l, 7);
       // silu(gate) * up -> down: tagged words in every group's copy, polled by every thread
-      phase_step([&] { gu_publish(&x->m[par][0][0], wg, G, lds, e); },
-                 [&] { down_load(wd, w, wg, G, true); }, MQ_NOTHING);
+      phase_step([&] { gu_publish(&x->m[par][0][0], rw, G, lds, e); },
+                 [&] { down_load(wd, w, rw, G, true); }, MQ_NOTHING);
       m_input_all(x->m[par][copy], lds + LDS_IN, (int)xtag(e), sy);
-      stamp(p, wg, l, 8);
-      down_run(wd, w, wg, G, lds);
-      stamp(p, wg, l, 9);
+      stamp(p, rw, l, 8);
+      down_run(wd, w, rw, G, lds);
+      stamp(p, rw, l, 9);
       // layer output -> next layer (or the LM head): epoch words
       phase_step(
           [&] {
             float res = lane_id() < nrh ? lds[LDS_A + r0h + lane_id()] : 0.f;
-            down_publish(wg, G, lds, res, [](int, float) {});
+            down_publish(rw, G, lds, res, [](int, float) {});
             hidden_publish(p, l, r0h, nrh, res, e);
           },
           [&] {
@@ -1640,13 +1696,14 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
               if constexpr (EARLY) k_early(l + 1);
             }
           },
-          [&] { hidden_gather(lds + LDS_IN, lds + LDS_HID, x->h[par][copy], e, sy); });
-      stamp(p, wg, l, 10);
+          MQ_NOTHING);
+      hidden_input_all(lds + LDS_IN, lds + LDS_HID, x->h[par][copy], e, sy);
+      stamp(p, rw, l, 10);
     }
     const bool more = step + 1 < p.nsteps;
-    lm_head_run(p, wg, G, lds, p.tok_out + step, p.nsteps == 1 ? p.logits : nullptr, pos, true,
+    lm_head_run(p, rw, G, lds, p.tok_out + step, p.nsteps == 1 ? p.logits : nullptr, pos, true,
                 false, more, epoch0 + (uint32_t)step + 1, true,
-                mq_xep_advance(xep0, (uint64_t)(step + 1) * (uint32_t)p.num_layers));
+                mq_xep_advance(xep0, (uint64_t)(step + 1) * (uint32_t)p.num_layers), !more);
     if (more) {
       // the next step's first weights do not depend on its token: in flight during the wait
       if (p.num_layers > 0) gqkv_load(wq, lds_layer(s_layers, 0), h, j, NG, true);
@@ -2291,6 +2348,7 @@ __global__ void mq_fill_state_kernel(MqState* st, int pos, int clear_err) {
     st->pos.v = (uint32_t)pos;
     st->steps.v = 0;
   }
+  if (t < MQ_GROUPS) st->place[t].v = 0;
 }
 // Debug: the exchange-epoch base (validated by the caller: xep < MQ_XEP_PERIOD).
 __global__ void mq_set_xep_kernel(MqState* st, uint32_t xep) {

@@ -96,6 +96,8 @@ struct MqState {
   MqLine xep;                  // exchange-epoch base in [0, MQ_XEP_PERIOD): advanced by
                                // mq_xep_advance(xep, num_layers) per decode step of either mode;
                                // creation and reset, which clear MqExchange, zero it
+  MqLine place[MQ_GROUPS];     // persistent launches: workgroups claimed on each XCD so far in
+                               // this launch (reset by its last step, and by every state fill)
 };
 
 struct MqDecodeParams {

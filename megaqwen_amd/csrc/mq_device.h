@@ -230,6 +230,28 @@ MQ_DEV void st_coh64(uint64_t* p, uint64_t v) {
 }
 MQ_DEV void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
+// ------------------------------------------------------------------ XCD-local exchange
+// Values exchanged only among workgroups of one XCD are stored with plain stores (no cache-
+// bypass bits): the per-CU vector L1 is write-through, so the store lands in the XCD's L2 and
+// stays there; the readers' agent-scope (sc1) loads above miss their own L1 and are served by
+// that L2.  A device-scope (sc1) store also writes through to memory, which the reader does not
+// need: measured on 256 co-resident workgroups exchanging one word per round inside their XCD,
+// 0.49 us per round against 0.79 us with sc1 stores (512 words per group: 1.6 against 3.4 us).
+// Readers on another XCD would not see these stores (their L2 may hold the line and the data
+// never reaches memory before the kernel ends), so the kernels that use them assign workgroup
+// roles from the hardware XCD index (xcc_id).  Workgroup-scope (sc0) loads are no substitute
+// for the sc1 loads: they are served by the reader's own L1 and never observe another CU's
+// stores.  The stores are single 64-bit (or 32-bit) instructions, so a word and its epoch or
+// tag arrive together.
+MQ_DEV void st_local64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+MQ_DEV void st_local32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+// Hardware XCD index of the executing workgroup (HW_REG_XCC_ID, bits 3:0).
+MQ_DEV int xcc_id() { return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11)) & 15; }
+
 // ---------------------------------------------------------------------------- sync state
 // Sync state lives in its own 128-byte lines (one L2 line each on gfx950).
 struct alignas(128) MqLine {
