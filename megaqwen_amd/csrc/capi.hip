@@ -49,7 +49,7 @@ Layout layout_of(const mq_model_desc* d) {
   L.prefill = align_up(L.xch + sizeof(MqExchange), 256);
   L.fused = align_up(L.prefill + mq_prefill_workspace_bytes(d->max_prefill_len), 256);
   // the fused short-prompt prefill's fp32 buffers (only for decoders that can prefill)
-  L.total = align_up(L.fused + (d->max_prefill_len > 0 ? mq_fused_workspace_bytes() : 0), 256);
+  L.total = align_up(L.fused + (d->max_prefill_len > 0 ? mq_fused_workspace_bytes(d->num_layers) : 0), 256);
   return L;
 }
 
@@ -226,7 +226,7 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   dec->ws = ws;
   mq_prefill_bind(&dec->pf, ws + lay.prefill, desc->max_prefill_len);
   memset(&dec->fused, 0, sizeof(dec->fused));
-  if (desc->max_prefill_len > 0) mq_fused_bind(&dec->fused, ws + lay.fused);
+  if (desc->max_prefill_len > 0) mq_fused_bind(&dec->fused, ws + lay.fused, desc->num_layers);
   if (mq_launch_clear_state(p.st, p.x, nullptr) != 0 ||
       (dec->pf.cnt != nullptr && mq_launch_zero(dec->pf.cnt, dec->pf.cnt_bytes, nullptr) != 0) ||
       hipStreamSynchronize(nullptr) != hipSuccess) {

@@ -1992,14 +1992,17 @@ template <int K>
 struct FpTile {
   uint4 b[K / 256];
 };
+// `shared`: the tile is also loaded by other workgroups of this XCD in the same stage (plain
+// loads, so that its L2 serves them after the first); otherwise non-temporal.
 template <int K>
-MQ_DEV void fp_tile_load(FpTile<K>& t, const bf16_t* row0) {
+MQ_DEV void fp_tile_load(FpTile<K>& t, const bf16_t* row0, bool shared = false) {
   // after every store of the stage (fp_grid_sync counts these loads as the last ones issued)
   asm volatile("" ::: "memory");
   const int lane = lane_id(), wave = wave_id();
   const bf16_t* r = row0 + (size_t)(lane & 15) * K + 8 * (lane >> 4);
 #pragma unroll
-  for (int j = 0; j < K / 256; ++j) t.b[j] = ld_nt16(r + 32 * (wave + 8 * j));
+  for (int j = 0; j < K / 256; ++j)
+    t.b[j] = shared ? ld16(r + 32 * (wave + 8 * j)) : ld_nt16(r + 32 * (wave + 8 * j));
 }
 
 // x = hi + mid + lo exactly, each part bf16: v_cvt_pk_bf16_f32 rounds to nearest even, and each
@@ -2026,51 +2029,66 @@ MQ_DEV void split3_bf16(const float (&x)[8], mq_bf16x8_t& hi, mq_bf16x8_t& mid, 
   lo = bf16x8_of(make_uint4(l[0], l[1], l[2], l[3]));
 }
 
-// One GEMM tile: C[r][c] = sum_k A[r][k] (* w_norm[k]) * W[c][k] for rows r < n of the fp32
-// input A (row stride K, device-coherent) and the NT weight tiles, then epi(row, col, v[NT])
-// for every row < n and the tile's 16 columns.  With NORM the values are scaled by the row's
+// One GEMM tile: C[r][c] = sum_k A[r][k] (* w_norm[k]) * W[c][k] for the rows r < n of 16-row
+// blocks rb0 .. rb0 + nbr - 1 (nbr <= 4) of the fp32 input A (row stride K; a buffer written
+// once per launch, read with plain loads) and the NT weight tiles, then
+// epi(row, col, v[NT], res) for every such row and the tile's 16 columns, where res = pre(row,
+// col) is loaded before the products (the residual of the O and down stages; 0 elsewhere), so
+// its round trip overlaps them.  With NORM the values are scaled by the row's
 // rsqrt(mean(A[r]^2) + eps) (the RMSNorm with weight w_norm).  All 512 threads take part.
-template <int K, bool NORM, int NT, class Epi>
-MQ_DEV void fp_gemm(const float* A, int n, const bf16_t* w_norm, const FpTile<K> (&t)[NT],
-                    float* lds, Epi epi) {
+template <int K, bool NORM, int NT, class Pre, class Epi>
+MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, const bf16_t* w_norm,
+                    const FpTile<K> (&t)[NT], float* lds, Pre pre, Epi epi) {
   const int lane = lane_id(), wave = wave_id();
-  const int nb = (n + 15) >> 4;
   // per-wave partials [NT][8 waves][4 blocks][16 rows][16 cols] and row sums [8][64]: C element
   // i of lane l is (row 4 (l / 16) + i, column l % 16) of the block
   float* part = lds;
   float* rs = lds + NT * 8 * 4 * 256;
+  // this thread's epilogue elements (idx = tid + 512 k) and their residuals, loaded first
+  float res[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int idx = tid() + MQ_THREADS * k, bl = idx >> 8, e = idx & 255;
+    const int row = 16 * (rb0 + bl) + (e >> 4);
+    res[k] = bl < nbr && row < n ? pre(row, e & 15) : 0.f;
+  }
+  // the norm weights of this wave's k-steps (the same for every block)
+  uint4 wn16[NORM ? K / 256 : 1];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < K / 256; ++j) wn16[j] = ld16(w_norm + 32 * (wave + 8 * j) + 8 * (lane >> 4));
+  }
   // 16-row blocks in batches of BB: all of a batch's input loads of this wave are issued before
-  // the first is used (one memory round trip per batch; the loads are device-coherent and slow
-  // to return).  Two blocks per batch for K = 1024 measured no faster than one at 64 positions
-  // (4.39 against 4.32 ms per prefill): the time goes to the volume of those loads, every
-  // workgroup reading all n input rows, not to their round trips.
+  // the first is used (one round trip per batch).
   constexpr int BB = 1;
-  for (int b0 = 0; b0 < nb; b0 += BB) {
+  for (int b0 = 0; b0 < nbr; b0 += BB) {
     // keeps the next batch's loads from being hoisted into this one (they would pin registers)
     asm volatile("" ::: "memory");
     uint64_t u[BB][K / 256][4];
 #pragma unroll
     for (int sb = 0; sb < BB; ++sb) {
-      const int row = 16 * (b0 + sb) + (lane & 15);
+      const int row = 16 * (rb0 + b0 + sb) + (lane & 15);
 #pragma unroll
       for (int j = 0; j < K / 256; ++j) {
-        const uint64_t* src = reinterpret_cast<const uint64_t*>(
-            A + (size_t)row * K + 32 * (wave + 8 * j) + 8 * (lane >> 4));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) u[sb][j][i] = row < n ? ld_coh64(src + i) : 0ull;
+        const float* src = A + (size_t)row * K + 32 * (wave + 8 * j) + 8 * (lane >> 4);
+        const uint4 a = row < n ? ld16(src) : make_uint4(0, 0, 0, 0);
+        const uint4 b = row < n ? ld16(src + 4) : make_uint4(0, 0, 0, 0);
+        u[sb][j][0] = (uint64_t)a.x | ((uint64_t)a.y << 32);
+        u[sb][j][1] = (uint64_t)a.z | ((uint64_t)a.w << 32);
+        u[sb][j][2] = (uint64_t)b.x | ((uint64_t)b.y << 32);
+        u[sb][j][3] = (uint64_t)b.z | ((uint64_t)b.w << 32);
       }
     }
 #pragma unroll
     for (int sb = 0; sb < BB; ++sb) {
       const int bb = b0 + sb;
-      if (bb >= nb) break;
+      if (bb >= nbr) break;
       mq_f32x4_t c[NT];
 #pragma unroll
       for (int q = 0; q < NT; ++q) c[q] = mq_f32x4_t{0.f, 0.f, 0.f, 0.f};
       float ss = 0.f;
 #pragma unroll
       for (int j = 0; j < K / 256; ++j) {
-        const int k0 = 32 * (wave + 8 * j) + 8 * (lane >> 4);
         float x[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -2079,7 +2097,7 @@ MQ_DEV void fp_gemm(const float* A, int n, const bf16_t* w_norm, const FpTile<K>
         }
         if constexpr (NORM) {
           float wn[8];
-          unpack8(ld16(w_norm + k0), wn);
+          unpack8(wn16[j], wn);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             ss = fmaf(x[e], x[e], ss);
@@ -2109,14 +2127,16 @@ MQ_DEV void fp_gemm(const float* A, int n, const bf16_t* w_norm, const FpTile<K>
     }
   }
   __syncthreads();
-  for (int idx = tid(); idx < nb * 256; idx += MQ_THREADS) {
-    const int bb = idx >> 8, e = idx & 255, row = 16 * bb + (e >> 4), col = e & 15;
-    if (row >= n) continue;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int idx = tid() + MQ_THREADS * k, bl = idx >> 8, e = idx & 255;
+    const int row = 16 * (rb0 + bl) + (e >> 4), col = e & 15;
+    if (bl >= nbr || row >= n) continue;
     float r = 1.f;
     if constexpr (NORM) {
       float s = 0.f;
 #pragma unroll
-      for (int w8 = 0; w8 < 8; ++w8) s += rs[w8 * 64 + row];
+      for (int w8 = 0; w8 < 8; ++w8) s += rs[w8 * 64 + 16 * bl + (e >> 4)];
       r = rsqrtf(s * (1.0f / K) + MQ_EPS);
     }
     float v[NT];
@@ -2124,78 +2144,102 @@ MQ_DEV void fp_gemm(const float* A, int n, const bf16_t* w_norm, const FpTile<K>
     for (int q = 0; q < NT; ++q) {
       float a = 0.f;
 #pragma unroll
-      for (int w8 = 0; w8 < 8; ++w8) a += part[((q * 8 + w8) * 4 + bb) * 256 + e];
+      for (int w8 = 0; w8 < 8; ++w8) a += part[((q * 8 + w8) * 4 + bl) * 256 + e];
       v[q] = NORM ? a * r : a;
     }
-    epi(row, col, v);
+    epi(row, col, v, res[k]);
   }
   __syncthreads();
 }
 
 // One row (128 dims, lane l: dims 2l, 2l + 1) of q or k: per-head RMSNorm with weight pair
-// `w2`, then rotate-half RoPE at position `pos` (prefill_mk_qk_norm_rope_cache,
+// `w2`, then rotate-half RoPE with this lane's table pairs c2, s2 of the row's position
+// (prefill_mk_qk_norm_rope_cache,
 // fused_prefill_megakernel_core.inl:186-325): o_d = x_d c_d - x_{d+64} s_d for d < 64,
 // o_d = x_{d-64} s_d + x_d c_d otherwise; the partner dims sit in lane l ^ 32.
-MQ_DEV float2 fp_norm_rope(float2 x, uint32_t w2, const MqDecodeParams& p, int pos) {
+MQ_DEV float2 fp_norm_rope(float2 x, uint32_t w2, uint32_t c2, uint32_t s2) {
   const int lane = lane_id();
   const float sc = rsqrtf(wave_sum(x.x * x.x + x.y * x.y) * (1.0f / MQ_D) + MQ_EPS);
   const float n0 = x.x * sc * bf16_lo(w2), n1 = x.y * sc * bf16_hi(w2);
   const float2 s0 = swap32(n0), s1 = swap32(n1);
   const float p0 = lane < 32 ? s0.y : s0.x, p1 = lane < 32 ? s1.y : s1.x;
-  const uint32_t c2 = ld32(p.cos + (size_t)pos * MQ_D + 2 * lane);
-  const uint32_t s2 = ld32(p.sin + (size_t)pos * MQ_D + 2 * lane);
   if (lane < 32)
     return make_float2(n0 * bf16_lo(c2) - p0 * bf16_lo(s2), n1 * bf16_hi(c2) - p1 * bf16_hi(s2));
   return make_float2(p0 * bf16_lo(s2) + n0 * bf16_lo(c2), p1 * bf16_hi(s2) + n1 * bf16_hi(c2));
 }
 
-// Attention item (kv head h, query block qb = positions 16 qb .. 16 qb + 15) of layer `layer`
-// (prefill_mk_causal_attention, fused_prefill_megakernel_core.inl:328-414): both query heads
-// 2h, 2h + 1 of the block against keys 0 .. min(n, 16 qb + 16) - 1, fp32 throughout (the keys
-// normalised and rotated here from the raw q|k|v rows; the block's own positions' K/V rows are
-// also written to the bf16 cache).  Scores use the reference's scale and expf softmax.
+// Attention item (kv head h, query block qb = positions FP_QB qb .. FP_QB qb + FP_QB - 1) of
+// layer `layer` (prefill_mk_causal_attention, fused_prefill_megakernel_core.inl:328-414): both
+// query heads 2h, 2h + 1 of the block against keys 0 .. min(n, FP_QB (qb + 1)) - 1, fp32
+// throughout (the keys normalised and rotated here from the raw q|k|v rows; the block's own
+// positions' K/V rows are also written to the bf16 cache).  Scores use the reference's scale and
+// an expf softmax.  Wave r holds query row r (position q0 + r / 2, head 2h + r % 2): lane j
+// scores key j (the q row is an LDS broadcast), the softmax is a wave reduction, and in P.V
+// lane l accumulates dims 2l, 2l + 1 over the keys in order.
+#define FP_QB 4
+MQ_DEV float2 ldf2(const float* p) {
+  const uint64_t u = *gptr<uint64_t>(p);
+  return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
+}
 MQ_DEV void fp_attention(const MqDecodeParams& p, const MqFusedArgs& f, const MqLayerW& w,
-                         int layer, int h, int qb, float* lds) {
+                         int layer, int h, int qb, const float* qkv, float* att, float* lds) {
+  static_assert(2 * FP_QB == MQ_WAVES, "one query row per wave");
+  static_assert(MQ_FUSED_MAX_N <= 64, "one key per lane");
   float* Ks = lds;                       // [64][FPA_S] keys after norm + RoPE
   float* Vs = lds + 64 * FPA_S;          // [64][FPA_S] values
-  float* Qs = lds + 128 * FPA_S;         // [32][FPA_S] rows r = 2 (i - q0) + (query head - 2h)
-  float* Ps = lds + 160 * FPA_S;         // [32][64] softmax weights
-  float* Ls = Ps + 32 * 64;              // [32] 1 / sum of the weights
-  const int n = f.n, q0 = 16 * qb, kn = min(n, q0 + 16), qn = kn - q0;
+  float* Qs = lds + 128 * FPA_S;         // [8][FPA_S] query rows after norm + RoPE
+  float* Ps = lds + 136 * FPA_S;         // [8][64] softmax weights
+  const int n = f.n, q0 = FP_QB * qb, kn = min(n, q0 + FP_QB), qn = kn - q0;
   const int lane = lane_id(), wave = wave_id();
   constexpr int QKV = MQ_QDIM + 2 * MQ_KVDIM;
   const uint32_t kw = ld32(w.k_norm + 2 * lane), qw = ld32(w.q_norm + 2 * lane);
   bf16_t* kc = p.kc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
   bf16_t* vc = p.vc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
-  for (int j = wave; j < kn; j += MQ_WAVES) {
-    const float* row = f.qkv + (size_t)j * QKV;
-    const float2 kr = ld_coh2(row + MQ_QDIM + h * MQ_D + 2 * lane);
-    const float2 vr = ld_coh2(row + MQ_QDIM + MQ_KVDIM + h * MQ_D + 2 * lane);
-    const float2 k = fp_norm_rope(kr, kw, p, j);
-    reinterpret_cast<float2*>(Ks + j * FPA_S)[lane] = k;
-    reinterpret_cast<float2*>(Vs + j * FPA_S)[lane] = vr;
-    if (j >= q0) {
-      reinterpret_cast<uint32_t*>(kc + (size_t)j * MQ_D)[lane] =
-          (uint32_t)f32_to_bf16(k.x) | ((uint32_t)f32_to_bf16(k.y) << 16);
-      reinterpret_cast<uint32_t*>(vc + (size_t)j * MQ_D)[lane] =
-          (uint32_t)f32_to_bf16(vr.x) | ((uint32_t)f32_to_bf16(vr.y) << 16);
+  // key rows j = wave + 8 i and this wave's query row: every load of the wave (raw rows and
+  // their RoPE table pairs) is issued before the first is used, one round trip in all
+  constexpr int KI = MQ_FUSED_MAX_N / MQ_WAVES;
+  float2 kr[KI], vr[KI], qr = make_float2(0.f, 0.f);
+  uint32_t kc2[KI], ks2[KI], qc2 = 0, qs2 = 0;
+  const int r = wave, pi = q0 + (r >> 1);        // this wave's query row and its position
+  const bool has_q = r < 2 * qn;
+#pragma unroll
+  for (int i = 0; i < KI; ++i) {
+    const int j = wave + MQ_WAVES * i;
+    if (j < kn) {
+      const float* row = qkv + (size_t)j * QKV;
+      kr[i] = ldf2(row + MQ_QDIM + h * MQ_D + 2 * lane);
+      vr[i] = ldf2(row + MQ_QDIM + MQ_KVDIM + h * MQ_D + 2 * lane);
+      kc2[i] = ld32(p.cos + (size_t)j * MQ_D + 2 * lane);
+      ks2[i] = ld32(p.sin + (size_t)j * MQ_D + 2 * lane);
     }
   }
-  for (int r = wave; r < 2 * qn; r += MQ_WAVES) {
-    const int i = q0 + (r >> 1), hq = 2 * h + (r & 1);
-    const float2 qr = ld_coh2(f.qkv + (size_t)i * QKV + hq * MQ_D + 2 * lane);
-    reinterpret_cast<float2*>(Qs + r * FPA_S)[lane] = fp_norm_rope(qr, qw, p, i);
+  if (has_q) {
+    qr = ldf2(qkv + (size_t)pi * QKV + (2 * h + (r & 1)) * MQ_D + 2 * lane);
+    qc2 = ld32(p.cos + (size_t)pi * MQ_D + 2 * lane);
+    qs2 = ld32(p.sin + (size_t)pi * MQ_D + 2 * lane);
   }
-  __syncthreads();
-  // scores: 16 threads per row r (a 16-lane DPP row), keys jj, jj + 16, jj + 32, jj + 48
-  const int r = tid() >> 4, jj = tid() & 15, i = q0 + (r >> 1);
-  const float scale = rsqrtf((float)MQ_D);
-  float s[4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int j = jj + 16 * m;
-    s[m] = -INFINITY;
-    if (r < 2 * qn && j < kn && j <= i) {
+  for (int i = 0; i < KI; ++i) {
+    const int j = wave + MQ_WAVES * i;
+    if (j < kn) {
+      const float2 k = fp_norm_rope(kr[i], kw, kc2[i], ks2[i]);
+      reinterpret_cast<float2*>(Ks + j * FPA_S)[lane] = k;
+      reinterpret_cast<float2*>(Vs + j * FPA_S)[lane] = vr[i];
+      if (j >= q0) {
+        reinterpret_cast<uint32_t*>(kc + (size_t)j * MQ_D)[lane] =
+            (uint32_t)f32_to_bf16(k.x) | ((uint32_t)f32_to_bf16(k.y) << 16);
+        reinterpret_cast<uint32_t*>(vc + (size_t)j * MQ_D)[lane] =
+            (uint32_t)f32_to_bf16(vr[i].x) | ((uint32_t)f32_to_bf16(vr[i].y) << 16);
+      }
+    }
+  }
+  if (has_q) reinterpret_cast<float2*>(Qs + r * FPA_S)[lane] = fp_norm_rope(qr, qw, qc2, qs2);
+  __syncthreads();
+  if (has_q) {
+    // scores of keys j = lane <= pi (causal), the reference's scale
+    const int j = lane;
+    float s = -INFINITY;
+    if (j < kn && j <= pi) {
       float acc = 0.f;
       const float4* qv = reinterpret_cast<const float4*>(Qs + r * FPA_S);
       const float4* kv = reinterpret_cast<const float4*>(Ks + j * FPA_S);
@@ -2207,43 +2251,24 @@ MQ_DEV void fp_attention(const MqDecodeParams& p, const MqFusedArgs& f, const Mq
         acc = fmaf(a.z, b.z, acc);
         acc = fmaf(a.w, b.w, acc);
       }
-      s[m] = acc * scale;
+      s = acc * rsqrtf((float)MQ_D);
     }
-  }
-  const float mx = row16_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-  float lsum = 0.f;
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const float e = s[m] == -INFINITY ? 0.f : expf(s[m] - mx);
-    Ps[r * 64 + jj + 16 * m] = e;
-    lsum += e;
-  }
-  lsum = row16_sum(lsum);
-  if (jj == 0) Ls[r] = 1.0f / lsum;
-  __syncthreads();
-  // P.V: thread (r, jj) owns dims 8 jj .. 8 jj + 7 of row r
-  if (r < 2 * qn) {
-    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j <= i; ++j) {
-      const float pw = Ps[r * 64 + j];
-      const float4 v0 = reinterpret_cast<const float4*>(Vs + j * FPA_S + 8 * jj)[0];
-      const float4 v1 = reinterpret_cast<const float4*>(Vs + j * FPA_S + 8 * jj)[1];
-      o[0] = fmaf(pw, v0.x, o[0]);
-      o[1] = fmaf(pw, v0.y, o[1]);
-      o[2] = fmaf(pw, v0.z, o[2]);
-      o[3] = fmaf(pw, v0.w, o[3]);
-      o[4] = fmaf(pw, v1.x, o[4]);
-      o[5] = fmaf(pw, v1.y, o[5]);
-      o[6] = fmaf(pw, v1.z, o[6]);
-      o[7] = fmaf(pw, v1.w, o[7]);
+    const float mx = wave_max(s);
+    const float e = s == -INFINITY ? 0.f : expf(s - mx);
+    const float inv = 1.0f / wave_sum(e);
+    Ps[r * 64 + j] = e;
+    // P.V (the weights just written by this wave: in-order LDS access within the wave)
+    float o0 = 0.f, o1 = 0.f;
+    const int jend = min(kn, pi + 1);
+    for (int jj = 0; jj < jend; ++jj) {
+      const float pw = Ps[r * 64 + jj];
+      const float2 v = reinterpret_cast<const float2*>(Vs + jj * FPA_S)[lane];
+      o0 = fmaf(pw, v.x, o0);
+      o1 = fmaf(pw, v.y, o1);
     }
-    const float inv = Ls[r];
-    float* dst = f.att + (size_t)i * MQ_QDIM + (2 * h + (r & 1)) * MQ_D + 8 * jj;
-#pragma unroll
-    for (int e = 0; e < 8; e += 2)
-      st_coh64(reinterpret_cast<uint64_t*>(dst + e),
-               (uint64_t)__float_as_uint(o[e] * inv) |
-                   ((uint64_t)__float_as_uint(o[e + 1] * inv) << 32));
+    st_coh64(reinterpret_cast<uint64_t*>(att + (size_t)pi * MQ_QDIM + (2 * h + (r & 1)) * MQ_D) +
+                 lane,
+             (uint64_t)__float_as_uint(o0 * inv) | ((uint64_t)__float_as_uint(o1 * inv) << 32));
   }
   __syncthreads();
 }
@@ -2264,6 +2289,11 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
   };
   using std::integral_constant;
   constexpr int QKV = MQ_QDIM + 2 * MQ_KVDIM;
+  // this launch's buffers: each written once, by one stage, and read after the next barrier
+  auto hbuf = [&](int i) { return f.h + (size_t)i * MQ_FUSED_MAX_N * MQ_H; };
+  auto qkvbuf = [&](int l) { return f.qkv + (size_t)l * MQ_FUSED_MAX_N * QKV; };
+  auto attbuf = [&](int l) { return f.att + (size_t)l * MQ_FUSED_MAX_N * MQ_QDIM; };
+  auto mbuf = [&](int l) { return f.m + (size_t)l * MQ_FUSED_MAX_N * MQ_I; };
   // embedding rows (prefill_mk_embedding, fused_prefill_megakernel_core.inl:3-33; the audio
   // rows as the kernel's patch step, :693-703); a token id outside the vocabulary reads row 0
   // and sets the error flag to 2
@@ -2277,31 +2307,49 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
     }
     const bf16_t* src = patched ? f.patch + (size_t)pr * MQ_H : p.embed + (size_t)tok * MQ_H;
     const uint32_t v = ld32(src + 2 * t);
-    st_coh64(reinterpret_cast<uint64_t*>(f.h + (size_t)row * MQ_H) + t,
+    st_coh64(reinterpret_cast<uint64_t*>(hbuf(0) + (size_t)row * MQ_H) + t,
              (uint64_t)__float_as_uint(bf16_lo(v)) | ((uint64_t)__float_as_uint(bf16_hi(v)) << 32));
   }
   const int nb = (n + 15) >> 4;
+  // The O and down stages have 1024 / 16 = 64 column tiles: with nb 16-row blocks, tile
+  // wg % 64 takes block wg / 64 in workgroup wg < 64 nb, so up to 256 workgroups share them (the
+  // four of a tile run on one XCD, wg % 8 = tile % 8, and share its weights through the L2).
+  const int hb_tile = wg % (MQ_H / 16), hb_rb = wg / (MQ_H / 16);
+  const bool hb_work = hb_rb < nb;
+  const bool hb_shared = nb > 1;
+  auto no_pre = [](int, int) { return 0.f; };
   FpTile<MQ_H> tq[1];
   const bool q_tile = wg < QKV / 16;
   if (p.num_layers > 0 && q_tile) fp_tile_load(tq[0], qkv_row(p.layers[0], 16 * wg));
   grid_sync(integral_constant<int, MQ_H / 256>(), p.num_layers > 0 && q_tile);
   for (int l = 0; l < p.num_layers; ++l) {
     const MqLayerW w = p.layers[l];
+    const float* hin = hbuf(2 * l);
+    float* hmid = hbuf(2 * l + 1);
+    float* hout = hbuf(2 * l + 2);
+    float* qkvl = qkvbuf(l);
+    float* attl = attbuf(l);
+    float* ml = mbuf(l);
     // q|k|v (prefill_mk_rmsnorm + prefill_mk_qkv_projection, :35-184)
     if (wg < QKV / 16)
-      fp_gemm<MQ_H, true, 1>(f.h, n, w.in_ln, tq, lds, [&](int row, int col, const float* v) {
-        st_coh(f.qkv + (size_t)row * QKV + 16 * wg + col, v[0]);
+      fp_gemm<MQ_H, true, 1>(hin, n, 0, nb, w.in_ln, tq, lds, no_pre,
+                             [&](int row, int col, const float* v, float) {
+        st_coh(qkvl + (size_t)row * QKV + 16 * wg + col, v[0]);
       });
     grid_sync(integral_constant<int, 0>(), false);
-    if (wg < MQ_NKV * nb) fp_attention(p, f, w, l, wg % MQ_NKV, wg / MQ_NKV, lds);
+    if (wg < MQ_NKV * ((n + FP_QB - 1) / FP_QB))
+      fp_attention(p, f, w, l, wg % MQ_NKV, wg / MQ_NKV, qkvl, attl, lds);
     FpTile<MQ_QDIM> to[1];
-    if (wg < MQ_H / 16) fp_tile_load(to[0], w.wo + (size_t)16 * wg * MQ_QDIM);
-    grid_sync(integral_constant<int, MQ_QDIM / 256>(), wg < MQ_H / 16);
+    if (hb_work) fp_tile_load(to[0], w.wo + (size_t)16 * hb_tile * MQ_QDIM, hb_shared);
+    grid_sync(integral_constant<int, MQ_QDIM / 256>(), hb_work);
     // O projection + residual (prefill_mk_o_proj_residual, :417-472)
-    if (wg < MQ_H / 16)
-      fp_gemm<MQ_QDIM, false, 1>(f.att, n, nullptr, to, lds, [&](int row, int col, const float* v) {
-        float* hp = f.h + (size_t)row * MQ_H + 16 * wg + col;
-        st_coh(hp, ld_coh(hp) + v[0]);
+    if (hb_work)
+      fp_gemm<MQ_QDIM, false, 1>(attl, n, hb_rb, 1, nullptr, to, lds,
+                                 [&](int row, int col) {
+                                   return *gptr<float>(hin + (size_t)row * MQ_H + 16 * hb_tile + col);
+                                 },
+                                 [&](int row, int col, const float* v, float res) {
+        st_coh(hmid + (size_t)row * MQ_H + 16 * hb_tile + col, res + v[0]);
       });
     FpTile<MQ_H> tgu[2];
     if (wg < MQ_I / 16) {
@@ -2311,24 +2359,28 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
     grid_sync(integral_constant<int, 2 * MQ_H / 256>(), wg < MQ_I / 16);
     // post RMSNorm + gate|up + silu(g) * u (prefill_mk_mlp_gate_up, :474-544)
     if (wg < MQ_I / 16)
-      fp_gemm<MQ_H, true, 2>(f.h, n, w.post_ln, tgu, lds, [&](int row, int col, const float* v) {
+      fp_gemm<MQ_H, true, 2>(hmid, n, 0, nb, w.post_ln, tgu, lds, no_pre,
+                             [&](int row, int col, const float* v, float) {
         const float g = v[0], u = v[1];
-        st_coh(f.m + (size_t)row * MQ_I + 16 * wg + col, g / (1.0f + expf(-g)) * u);
+        st_coh(ml + (size_t)row * MQ_I + 16 * wg + col, g / (1.0f + expf(-g)) * u);
       });
     FpTile<MQ_I> td[1];
-    if (wg < MQ_H / 16) fp_tile_load(td[0], w.wd + (size_t)16 * wg * MQ_I);
-    grid_sync(integral_constant<int, MQ_I / 256>(), wg < MQ_H / 16);
+    if (hb_work) fp_tile_load(td[0], w.wd + (size_t)16 * hb_tile * MQ_I, hb_shared);
+    grid_sync(integral_constant<int, MQ_I / 256>(), hb_work);
     // down projection + residual (prefill_mk_mlp_down_residual, :546-599)
-    if (wg < MQ_H / 16)
-      fp_gemm<MQ_I, false, 1>(f.m, n, nullptr, td, lds, [&](int row, int col, const float* v) {
-        float* hp = f.h + (size_t)row * MQ_H + 16 * wg + col;
-        st_coh(hp, ld_coh(hp) + v[0]);
+    if (hb_work)
+      fp_gemm<MQ_I, false, 1>(ml, n, hb_rb, 1, nullptr, td, lds,
+                              [&](int row, int col) {
+                                return *gptr<float>(hmid + (size_t)row * MQ_H + 16 * hb_tile + col);
+                              },
+                              [&](int row, int col, const float* v, float res) {
+        st_coh(hout + (size_t)row * MQ_H + 16 * hb_tile + col, res + v[0]);
       });
     if (l + 1 < p.num_layers && q_tile) fp_tile_load(tq[0], qkv_row(p.layers[l + 1], 16 * wg));
     grid_sync(integral_constant<int, MQ_H / 256>(), l + 1 < p.num_layers && q_tile);
   }
   // final RMSNorm of the last position (fp32, prefill_mk_final_norm, :601-650) + LM head argmax
-  const float2 hv = ld_coh2(f.h + (size_t)(n - 1) * MQ_H + 2 * t);
+  const float2 hv = ldf2(hbuf(2 * p.num_layers) + (size_t)(n - 1) * MQ_H + 2 * t);
   lds[LDS_IN + 2 * t] = hv.x;
   lds[LDS_IN + 2 * t + 1] = hv.y;
   __syncthreads();
@@ -2400,17 +2452,20 @@ static int launch_status() {
   return e == hipSuccess ? 0 : -(int)e - 1000;
 }
 
-size_t mq_fused_workspace_bytes() {
-  return (size_t)MQ_FUSED_MAX_N * (MQ_H + MQ_QDIM + 2 * MQ_KVDIM + MQ_QDIM + MQ_I) * 4 +
+size_t mq_fused_workspace_bytes(int num_layers) {
+  const size_t L = (size_t)(num_layers > 0 ? num_layers : 0);
+  return (size_t)MQ_FUSED_MAX_N * 4 *
+             ((2 * L + 1) * MQ_H + L * (MQ_QDIM + 2 * MQ_KVDIM + MQ_QDIM + MQ_I)) +
          FP_STRIPES * 128;
 }
-void mq_fused_bind(MqFusedArgs* f, char* base) {
+void mq_fused_bind(MqFusedArgs* f, char* base, int num_layers) {
+  const size_t L = (size_t)(num_layers > 0 ? num_layers : 0);
   float* q = reinterpret_cast<float*>(base);
   f->h = q;
-  f->qkv = f->h + MQ_FUSED_MAX_N * MQ_H;
-  f->att = f->qkv + MQ_FUSED_MAX_N * (MQ_QDIM + 2 * MQ_KVDIM);
-  f->m = f->att + MQ_FUSED_MAX_N * MQ_QDIM;
-  f->bar = reinterpret_cast<uint32_t*>(f->m + MQ_FUSED_MAX_N * MQ_I);
+  f->qkv = f->h + (2 * L + 1) * MQ_FUSED_MAX_N * MQ_H;
+  f->att = f->qkv + L * MQ_FUSED_MAX_N * (MQ_QDIM + 2 * MQ_KVDIM);
+  f->m = f->att + L * MQ_FUSED_MAX_N * MQ_QDIM;
+  f->bar = reinterpret_cast<uint32_t*>(f->m + L * MQ_FUSED_MAX_N * MQ_I);
 }
 static int g_fused_blocks_per_cu = -1;
 int mq_launch_prefill_fused(const MqDecodeParams& p, const MqFusedArgs& f, int grid,

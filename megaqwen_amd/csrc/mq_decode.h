@@ -163,13 +163,20 @@ __host__ __device__ inline int mq_attn_chunk_len(int cache_len, int nch) {
 int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t stream);
 
 // Fused short-prompt prefill (mq_prefill_fused_kernel): fp32 buffers for up to
-// MQ_FUSED_MAX_N positions, in the decoder workspace (mq_fused_workspace_bytes).
+// MQ_FUSED_MAX_N positions, in the decoder workspace (mq_fused_workspace_bytes).  Every
+// activation of a launch has a buffer of its own (one per layer and stage), written once and
+// read only after the grid barrier that follows its writes: no cache can then hold a stale copy
+// of a line a reader loads (caches start a kernel clean, and no line is read before it is
+// written), so readers use plain loads, served by their XCD's L2 after its first miss, instead
+// of device-coherent loads that each go to memory.
 #define MQ_FUSED_MAX_N 64
 struct MqFusedArgs {
-  float* h;                    // [MQ_FUSED_MAX_N][H] residual stream
-  float* qkv;                  // [MQ_FUSED_MAX_N][4096] raw q | k | v projections
-  float* att;                  // [MQ_FUSED_MAX_N][2048] attention output
-  float* m;                    // [MQ_FUSED_MAX_N][I] silu(gate) * up
+  float* h;                    // [2 L + 1][MQ_FUSED_MAX_N][H] residual stream: the embeddings,
+                               // then per layer l the stream after attention (2 l + 1) and
+                               // after the MLP (2 l + 2)
+  float* qkv;                  // [L][MQ_FUSED_MAX_N][4096] raw q | k | v projections
+  float* att;                  // [L][MQ_FUSED_MAX_N][2048] attention output
+  float* m;                    // [L][MQ_FUSED_MAX_N][I] silu(gate) * up
   uint32_t* bar;               // grid-barrier counter stripes (32 x 128 bytes), zeroed per launch
   const int32_t* tokens;       // device token ids [n]
   int n;
@@ -179,8 +186,8 @@ struct MqFusedArgs {
   int* tok_out;                // greedy next token
   float* logits;               // optional fp32 [vocab] of the last position
 };
-size_t mq_fused_workspace_bytes();
-void mq_fused_bind(MqFusedArgs* f, char* base);
+size_t mq_fused_workspace_bytes(int num_layers);
+void mq_fused_bind(MqFusedArgs* f, char* base, int num_layers);
 // One cooperative launch over `grid` (>= 256) workgroups; 1 <= f.n <= MQ_FUSED_MAX_N.
 int mq_launch_prefill_fused(const MqDecodeParams& p, const MqFusedArgs& f, int grid,
                             hipStream_t stream);
