@@ -2038,7 +2038,9 @@ MQ_DEV void split3_bf16(const float (&x)[8], mq_bf16x8_t& hi, mq_bf16x8_t& mid, 
 // rsqrt(mean(A[r]^2) + eps) (the RMSNorm with weight w_norm).  All 512 threads take part.
 template <int K, bool NORM, int NT, class Pre, class Epi>
 MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, const bf16_t* w_norm,
-                    const FpTile<K> (&t)[NT], float* lds, Pre pre, Epi epi) {
+                    const FpTile<K> (&t)[NT], float* lds, Pre pre, Epi epi, int row_lo = 0) {
+  // rows below row_lo are left to another workgroup (zero inputs, no outputs); block row i of
+  // block b is row 16 (rb0 + b) + i
   const int lane = lane_id(), wave = wave_id();
   // per-wave partials [NT][8 waves][4 blocks][16 rows][16 cols] and row sums [8][64]: C element
   // i of lane l is (row 4 (l / 16) + i, column l % 16) of the block
@@ -2050,7 +2052,7 @@ MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, const bf16_t* w_nor
   for (int k = 0; k < 2; ++k) {
     const int idx = tid() + MQ_THREADS * k, bl = idx >> 8, e = idx & 255;
     const int row = 16 * (rb0 + bl) + (e >> 4);
-    res[k] = bl < nbr && row < n ? pre(row, e & 15) : 0.f;
+    res[k] = bl < nbr && row >= row_lo && row < n ? pre(row, e & 15) : 0.f;
   }
   // the norm weights of this wave's k-steps (the same for every block)
   uint4 wn16[NORM ? K / 256 : 1];
@@ -2071,8 +2073,9 @@ MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, const bf16_t* w_nor
 #pragma unroll
       for (int j = 0; j < K / 256; ++j) {
         const float* src = A + (size_t)row * K + 32 * (wave + 8 * j) + 8 * (lane >> 4);
-        const uint4 a = row < n ? ld16(src) : make_uint4(0, 0, 0, 0);
-        const uint4 b = row < n ? ld16(src + 4) : make_uint4(0, 0, 0, 0);
+        const bool in = row >= row_lo && row < n;
+        const uint4 a = in ? ld16(src) : make_uint4(0, 0, 0, 0);
+        const uint4 b = in ? ld16(src + 4) : make_uint4(0, 0, 0, 0);
         u[sb][j][0] = (uint64_t)a.x | ((uint64_t)a.y << 32);
         u[sb][j][1] = (uint64_t)a.z | ((uint64_t)a.w << 32);
         u[sb][j][2] = (uint64_t)b.x | ((uint64_t)b.y << 32);
@@ -2131,7 +2134,7 @@ MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, const bf16_t* w_nor
   for (int k = 0; k < 2; ++k) {
     const int idx = tid() + MQ_THREADS * k, bl = idx >> 8, e = idx & 255;
     const int row = 16 * (rb0 + bl) + (e >> 4), col = e & 15;
-    if (bl >= nbr || row >= n) continue;
+    if (bl >= nbr || row < row_lo || row >= n) continue;
     float r = 1.f;
     if constexpr (NORM) {
       float s = 0.f;
@@ -2311,12 +2314,17 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
              (uint64_t)__float_as_uint(bf16_lo(v)) | ((uint64_t)__float_as_uint(bf16_hi(v)) << 32));
   }
   const int nb = (n + 15) >> 4;
-  // The O and down stages have 1024 / 16 = 64 column tiles: with nb 16-row blocks, tile
-  // wg % 64 takes block wg / 64 in workgroup wg < 64 nb, so up to 256 workgroups share them (the
-  // four of a tile run on one XCD, wg % 8 = tile % 8, and share its weights through the L2).
-  const int hb_tile = wg % (MQ_H / 16), hb_rb = wg / (MQ_H / 16);
-  const bool hb_work = hb_rb < nb;
-  const bool hb_shared = nb > 1;
+  // The O and down stages have 1024 / 16 = 64 column tiles, each shared by four workgroups
+  // wg = tile + 64 part that take row groups of R = ceil(n / 4) rows (in the one or two 16-row
+  // MFMA blocks that hold them; the other block rows are zero), so every workgroup reads only its
+  // rows of the input.  The four of a tile run on one XCD (wg % 8 = tile % 8) and share its
+  // weights through the L2.
+  const int hb_tile = wg % (MQ_H / 16), hb_part = wg / (MQ_H / 16);
+  const int hb_rows = (n + 3) / 4;
+  const int hb_lo = hb_part * hb_rows, hb_hi = min(n, hb_lo + hb_rows), hb_rb = hb_lo / 16;
+  const int hb_nb = hb_hi > hb_lo ? (hb_hi - 1) / 16 - hb_rb + 1 : 0;
+  const bool hb_work = hb_lo < n;
+  const bool hb_shared = n > hb_rows;
   auto no_pre = [](int, int) { return 0.f; };
   FpTile<MQ_H> tq[1];
   const bool q_tile = wg < QKV / 16;
@@ -2344,13 +2352,13 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
     grid_sync(integral_constant<int, MQ_QDIM / 256>(), hb_work);
     // O projection + residual (prefill_mk_o_proj_residual, :417-472)
     if (hb_work)
-      fp_gemm<MQ_QDIM, false, 1>(attl, n, hb_rb, 1, nullptr, to, lds,
+      fp_gemm<MQ_QDIM, false, 1>(attl, hb_hi, hb_rb, hb_nb, nullptr, to, lds,
                                  [&](int row, int col) {
                                    return *gptr<float>(hin + (size_t)row * MQ_H + 16 * hb_tile + col);
                                  },
                                  [&](int row, int col, const float* v, float res) {
         st_coh(hmid + (size_t)row * MQ_H + 16 * hb_tile + col, res + v[0]);
-      });
+      }, hb_lo);
     FpTile<MQ_H> tgu[2];
     if (wg < MQ_I / 16) {
       fp_tile_load(tgu[0], w.wg + (size_t)16 * wg * MQ_H);
@@ -2369,13 +2377,13 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
     grid_sync(integral_constant<int, MQ_I / 256>(), hb_work);
     // down projection + residual (prefill_mk_mlp_down_residual, :546-599)
     if (hb_work)
-      fp_gemm<MQ_I, false, 1>(ml, n, hb_rb, 1, nullptr, td, lds,
+      fp_gemm<MQ_I, false, 1>(ml, hb_hi, hb_rb, hb_nb, nullptr, td, lds,
                               [&](int row, int col) {
                                 return *gptr<float>(hmid + (size_t)row * MQ_H + 16 * hb_tile + col);
                               },
                               [&](int row, int col, const float* v, float res) {
         st_coh(hout + (size_t)row * MQ_H + 16 * hb_tile + col, res + v[0]);
-      });
+      }, hb_lo);
     if (l + 1 < p.num_layers && q_tile) fp_tile_load(tq[0], qkv_row(p.layers[l + 1], 16 * wg));
     grid_sync(integral_constant<int, MQ_H / 256>(), l + 1 < p.num_layers && q_tile);
   }
