@@ -95,14 +95,17 @@ struct RowSet {
   static_assert(KS % 512 == 0, "segments are whole 512-element wave loads");
   uint4 w[PF][NL];
 
+  // fixed: items past the row count load row 0 instead of zeros (their totals are never handed
+  // out), so the number of loads after earlier ones is known to the compiler
   template <class RowPtr>
-  MQ_DEV void load(RowPtr rowptr, int nr, bool paced = false) {
+  MQ_DEV void load(RowPtr rowptr, int nr, bool paced = false, bool fixed = false) {
     const int lane = lane_id(), wave = wave_id();
     if (wave >= MQ_CWAVES) return;
     const int nitems = nr * S;
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      const int it = wave + j * MQ_CWAVES;
+      const int it0 = wave + j * MQ_CWAVES;
+      const int it = fixed && it0 >= nitems ? 0 : it0;
       if (it < nitems) {
         const bf16_t* r = rowptr(it / S) + (it % S) * KS + lane * 8;
 #pragma unroll
@@ -925,12 +928,12 @@ MQ_DEV void o_publish(float* a_out, int wg, int G, const float* lds, float& res)
 
 // ------------------------------------------------------------------------- P4: gate / up
 MQ_DEV void gu_load(GateUpSet& ws, const MqLayerW& w, int wg, int G,
-                    bool paced = false) {
+                    bool paced = false, bool fixed = false) {
   int r0, nr;
   row_range(MQ_I, wg, G, r0, nr);
   ws.load([&](int i) {
     return i < nr ? w.wg + (size_t)(r0 + i) * MQ_H : w.wu + (size_t)(r0 + i - nr) * MQ_H;
-  }, 2 * nr, paced);
+  }, 2 * nr, paced, fixed);
 }
 // Input: a in LDS_IN; gate and up dot products -> LDS_PR.
 MQ_DEV void gu_run(const GateUpSet& ws, const MqLayerW& w, int wg, int G, float* lds) {
@@ -1636,16 +1639,26 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
                 gu_load(wgu, w, rw, G, true);
               } else {
                 kv_load_v<true>(kv, kv_base(p.vc, p, l, h), kv0, kv1, pos, kv_dummy);
-                if (ga.local) opart_load(wo, w, h, j, NG);
+                if (ga.local) {
+                  opart_load(wo, w, h, j, NG);
+                  gu_load(wgu, w, rw, G, true, true);
+                }
               }
             } else {
               if (!ga.active) {
                 gu_load(wgu, w, rw, G, true);
+              } else if (ga.local) {
+                // local mode: no exchange follows the attention, so the O rows go now, and the
+                // gate|up weights too, landing during the attention instead of during the
+                // O-partial exchange; fixed load counts keep the compiler's wait for the K/V
+                // rows from waiting for them
+                kv_block_load<true>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), kv0,
+                                    kv1, pos, kv_dummy);
+                opart_load(wo, w, h, j, NG);
+                gu_load(wgu, w, rw, G, true, true);
               } else {
                 kv_block_load<false>(kv, kv_base(p.kc, p, l, h), kv_base(p.vc, p, l, h), kv0,
                                      kv1, pos, kv_dummy);
-                // local mode: no exchange follows the attention, so the O rows go now
-                if (ga.local) opart_load(wo, w, h, j, NG);
               }
             }
           },
@@ -1671,7 +1684,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_decode_persistent_kernel(MqDeco
                    // local mode: the new position's K/V row (ALDS_KN/VN are still intact)
                    if (ga.local && ga.has_pos) attn_cache_row(p, l, h, pos, lds);
                  },
-                 [&] { if (ga.active) gu_load(wgu, w, rw, G, true); }, MQ_NOTHING);
+                 [&] { if (ga.active && !ga.local) gu_load(wgu, w, rw, G, true); }, MQ_NOTHING);
       gu_input_all(&x->opart[par][copy][0][0], lds, (int)xtag(e), sy);
       stamp(p, rw, l, 6);
       gu_run(wgu, w, rw, G, lds);
