@@ -25,8 +25,13 @@ FLAGS = [
 
 
 # decode.hip's kernels hold up to 256 VGPRs (two waves per SIMD); a spill there is silent and
-# costs ~15% of a decode step, so its compile reports per-kernel resource usage to this file
+# costs ~15% of a decode step, so every compile reports per-kernel resource usage to
+# _build/<source>_resources.txt (decode.hip's is RESOURCE_REPORT) and warns on a spill
 RESOURCE_REPORT = os.path.join(HERE, "_build", "decode_resources.txt")
+
+
+def resource_report(src: str) -> str:
+    return os.path.join(HERE, "_build", src.replace(".hip", "_resources.txt"))
 
 
 def parse_resource_usage(text: str) -> dict:
@@ -55,27 +60,23 @@ def build(verbose: bool = False) -> str:
     os.makedirs(os.path.join(HERE, "_build"), exist_ok=True)
     for src in SOURCES:
         obj = os.path.join(HERE, "_build", src.replace(".hip", ".o"))
-        cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
-        if src == "decode.hip":
-            cmd += ["-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics"]
+        cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj,
+               "-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics"]
         if verbose:
             print(" ".join(cmd), flush=True)
-        if src == "decode.hip":
-            r = subprocess.run(cmd, stderr=subprocess.PIPE, text=True)
-            remarks = [ln for ln in r.stderr.splitlines() if "kernel-resource-usage" in ln]
-            rest = [ln for ln in r.stderr.splitlines() if "kernel-resource-usage" not in ln]
-            if rest:
-                print("\n".join(rest), file=sys.stderr, flush=True)
-            if r.returncode != 0:
-                raise subprocess.CalledProcessError(r.returncode, cmd)
-            with open(RESOURCE_REPORT, "w") as f:
-                f.write("\n".join(remarks) + "\n")
-            for name, u in parse_resource_usage("\n".join(remarks)).items():
-                if u.get("VGPRs Spill", 0) or u.get("ScratchSize", 0):
-                    print(f"warning: {name} spills ({u.get('VGPRs Spill', 0)} VGPRs, "
-                          f"{u.get('ScratchSize', 0)} B scratch per lane)", file=sys.stderr)
-        else:
-            subprocess.run(cmd, check=True)
+        r = subprocess.run(cmd, stderr=subprocess.PIPE, text=True)
+        remarks = [ln for ln in r.stderr.splitlines() if "kernel-resource-usage" in ln]
+        rest = [ln for ln in r.stderr.splitlines() if "kernel-resource-usage" not in ln]
+        if rest:
+            print("\n".join(rest), file=sys.stderr, flush=True)
+        if r.returncode != 0:
+            raise subprocess.CalledProcessError(r.returncode, cmd)
+        with open(resource_report(src), "w") as f:
+            f.write("\n".join(remarks) + "\n")
+        for name, u in parse_resource_usage("\n".join(remarks)).items():
+            if u.get("VGPRs Spill", 0) or u.get("ScratchSize", 0):
+                print(f"warning: {name} spills ({u.get('VGPRs Spill', 0)} VGPRs, "
+                      f"{u.get('ScratchSize', 0)} B scratch per lane)", file=sys.stderr)
         objs.append(obj)
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", *objs, "-o", tmp]
