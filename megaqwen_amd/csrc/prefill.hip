@@ -565,6 +565,7 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(GemmArgs g) {
 // last block).  The kernel is held to 256 registers so that two waves share each SIMD: one
 // wave's softmax (VALU) runs while the other's MFMAs run.  K is loaded one tile ahead.
 #define ATT_SPLIT 4
+#define ATT_LAZY 8.0f          // running-max slack (log2 units): weights stay below 2^8
 #ifndef ATT_P_SPLIT
 #define ATT_P_SPLIT 1
 #endif
@@ -635,35 +636,57 @@ pf_attn_kernel(MqDecodeParams p, int layer, const bf16_t* __restrict__ qkv,
       const int key = k0 + 16 * (j >> 3) + 8 * hh + (j & 7);
       raw[j] = (!DIAG || key <= q) ? sacc[j] : -INFINITY;
     }
-    float mloc = fmaxf(raw[0], raw[1]);
+    float mloc = fmaxf(fmaxf(raw[0], raw[1]), raw[2]);
 #pragma unroll
-    for (int j = 2; j < 16; j += 2) mloc = fmaxf(mloc, fmaxf(raw[j], raw[j + 1]));
+    for (int j = 3; j < 15; j += 2) mloc = fmaxf(fmaxf(mloc, raw[j]), raw[j + 1]);
+    mloc = fmaxf(mloc, raw[15]);
     // max(raw) * scale == max(raw * scale): rounding is monotonic and scale > 0
-    const float m_new = fmaxf(m, max_xor32(mloc) * scale);
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-    m = m_new;
+    const float mt = max_xor32(mloc) * scale;
+    // Lazy running max: a lane takes the tile's max only when it exceeds the max its weights
+    // use by more than ATT_LAZY (log2 units), so the weights stay below 2^ATT_LAZY and o and l are
+    // rescaled only in the rare tiles where that happens (the result is the same softmax: o and l
+    // always share one reference max).  The first tile sets it (m = -inf).
+    if (__builtin_amdgcn_ballot_w64(mt > m + ATT_LAZY) != 0) {
+      const float m_new = mt > m + ATT_LAZY ? mt : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) o[nt][j] *= alpha;
+    }
+    // weights p = 2^(s scale - m) as bf16 hi + lo: hi is p rounded to bf16, lo the remainder
+    // p - hi (exact in fp32) rounded to bf16; two bf16 values per conversion
     float ls = 0.f;
+    uint32_t ph[2][4];
+#if ATT_P_SPLIT
+    uint32_t pl[2][4];
+#endif
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(raw[j], scale, -m));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(raw[j + 1], scale, -m));
+      ls += p0;
+      ls += p1;
+      const uint32_t hp = pack_bf16x2(p0, p1);
+      ph[j >> 3][(j & 7) >> 1] = hp;
+#if ATT_P_SPLIT
+      pl[j >> 3][(j & 7) >> 1] =
+          pack_bf16x2(p0 - __uint_as_float(hp << 16), p1 - __uint_as_float(hp & 0xffff0000u));
+#endif
+    }
+    l += ls;
     mq_bf16x8 phi[2];
 #if ATT_P_SPLIT
     mq_bf16x8 plo[2];
 #endif
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float pv = __builtin_amdgcn_exp2f(fmaf(raw[j], scale, -m_new));
-      ls += pv;
-      const __bf16 hb = (__bf16)pv;
-      phi[j >> 3][j & 7] = hb;
+    for (int s = 0; s < 2; ++s) {
+      phi[s] = as_bf16x8(make_uint4(ph[s][0], ph[s][1], ph[s][2], ph[s][3]));
 #if ATT_P_SPLIT
-      plo[j >> 3][j & 7] = (__bf16)(pv - (float)hb);
+      plo[s] = as_bf16x8(make_uint4(pl[s][0], pl[s][1], pl[s][2], pl[s][3]));
 #endif
-    }
-    l = l * alpha + ls;
-    // rescale only when some lane's max moved (alpha == 1 leaves o unchanged bit for bit)
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) o[nt][j] *= alpha;
     }
     if (DIAG && k0 + ATT_KT > n) {
       // keys >= n: their weights are 0, but the V^T padding may hold anything (0 * NaN)
