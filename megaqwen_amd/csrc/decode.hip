@@ -1154,8 +1154,8 @@ MQ_DEV void gqkv_publish(uint64_t* xq, uint32_t e, int j, int NG, const float* l
   }
 }
 
-// Position chunks of a group: as many chunks of at least one register slot (28 positions) as
-// the group has workgroups; chunk j = [p0, p1).  All chunks c < nch are non-empty.
+// Position chunks of a group: as many chunks of at least mq_attn_min_chunk positions as the group
+// has workgroups; chunk j = [p0, p1).  All chunks c < nch are non-empty.
 // Local mode (cache_len <= local_max): one chunk over all positions.  With `all_local` (the
 // persistent kernel) every workgroup of the group computes it, so the attention output needs no
 // exchange; otherwise (one kernel per phase) workgroup 0 of the group computes it and publishes
@@ -1177,7 +1177,8 @@ MQ_DEV GAttn gattn_plan(int j, int NG, int cache_len, int pos, int local_max, bo
     g.has_new = g.active;
     return g;
   }
-  const int want = (cache_len + MQ_ATT_SLOT - 1) / MQ_ATT_SLOT;
+  const int mc = mq_attn_min_chunk(cache_len);
+  const int want = (cache_len + mc - 1) / mc;
   const int n0 = min(min(NG, MQ_GROUP_CHUNKS), want);
   const int clen = (cache_len + n0 - 1) / n0;
   g.nch = (cache_len + clen - 1) / clen;

@@ -191,12 +191,22 @@ void mq_fused_bind(MqFusedArgs* f, char* base, int num_layers);
 // One cooperative launch over `grid` (>= 256) workgroups; 1 <= f.n <= MQ_FUSED_MAX_N.
 int mq_launch_prefill_fused(const MqDecodeParams& p, const MqFusedArgs& f, int grid,
                             hipStream_t stream);
+// Smallest split-mode attention chunk (positions) of a kv-head group for a cache length: each
+// chunk is a partial the whole group polls and merges, so below a few thousand positions fewer,
+// longer chunks pay (per token, A/B on one box, against chunks of at least 28: 1024 positions
+// 525.8 against 536.9 us with 56, 2048 positions 550.6 against 554.2 with 112; 300 positions
+// unchanged with 56, slower with 112).  Every chunk is at least one register slot per compute
+// wave (MQ_ATT_SLOT).
+__host__ __device__ inline int mq_attn_min_chunk(int cache_len) {
+  return cache_len < 1536 ? 2 * MQ_ATT_SLOT : 4 * MQ_ATT_SLOT;
+}
 // Whether a persistent launch starting at `pos` should use the long-context variant: every
 // workgroup of a group then holds an attention chunk in every step of the launch (positions
 // only grow within a launch), and the short-context local mode no longer applies.
 __host__ __device__ inline int mq_decode_early_kv(int pos, int grid, int local_max) {
   const int cache_len = pos + 1;
-  return cache_len >= (grid / MQ_GROUPS) * MQ_ATT_SLOT && cache_len > local_max ? 1 : 0;
+  return cache_len >= (grid / MQ_GROUPS) * mq_attn_min_chunk(cache_len) && cache_len > local_max
+             ? 1 : 0;
 }
 // Clears the completion state and sets the device position; the error flag is kept
 // (sticky until mq_decoder_reset or creation, so mq_decoder_check still reports it) unless

@@ -145,9 +145,9 @@ def test_decode_long_context_chunks(small):
 
 @pytest.mark.parametrize("ctx", [2000, 7300])
 def test_decode_long_chunks_after_prefill(ctx):
-    """Contexts where the per-group attention chunks exceed one register slot (28 positions:
-    cache_len > 896, the seven-wave path) and one 224-position block (cache_len > 7168, several
-    blocks per chunk).  The prompt is prefilled on the GPU; the oracle takes over the GPU's KV
+    """Contexts split into long per-group attention chunks (2000 positions: 18 chunks of 112,
+    mq_attn_min_chunk) and into chunks longer than one 224-position block (7300 positions: 32
+    chunks of 229, several blocks per chunk).  The prompt is prefilled on the GPU; the oracle takes over the GPU's KV
     cache, so the decode steps are compared on identical caches (teacher-forced, 2e-2), in both
     decode modes."""
     dec, orc, sp, _ = build_pair(2, 151936, ctx + 16, seed=6, norm_jitter=0.1, max_prefill=ctx)
