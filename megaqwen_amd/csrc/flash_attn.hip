@@ -102,7 +102,9 @@ __global__ void __launch_bounds__(256) fa_pack_kernel(const uint16_t* __restrict
   }
 }
 
-template <bool F16>
+// CPOS: the scale is >= 0 (the softmax max is taken over the raw scores; otherwise their min),
+// a compile-time choice so that a tile carries neither the other extreme nor selects between them
+template <bool F16, bool CPOS>
 __global__ void __launch_bounds__(64 * FA_WAVES) __attribute__((amdgpu_waves_per_eu(3)))
 fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint4* __restrict__ kp,
                const uint4* __restrict__ vp, uint16_t* __restrict__ out, int T,
@@ -147,14 +149,14 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint4* __restrict__ kp,
   // compiler wait for every outstanding load at the next use of any of them.
   const uint4* KP = kp + (size_t)bh * ntiles * 256 + lane;
   const uint4* VP = vp + (size_t)bh * ntiles * 256 + lane;
-  uint4 kr[4], vr[4];
+  uint4 kr[4];
   auto load_k = [&](int t) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) kr[s] = ld16(KP + (size_t)t * 256 + 64 * s);
   };
-  auto load_v = [&](int t) {
+  auto load_v = [&](int t, uint4 (&v)[4]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vr[i] = ld16(VP + (size_t)t * 256 + 64 * i);
+    for (int i = 0; i < 4; ++i) v[i] = ld16(VP + (size_t)t * 256 + 64 * i);
   };
   // S^T of the tile whose K operand is in kr
   auto scores = [&]() {
@@ -178,27 +180,27 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint4* __restrict__ kp,
   float m = -INFINITY, l = 0.f;
   // max_j (s_j * c) is max_j(s_j) * c for c >= 0 and min_j(s_j) * c for c < 0 (rounding is
   // monotonic), so the extreme is taken over the raw scores
-  const bool cpos = scale_log2 >= 0.f;
 
   // Software pipeline: the MFMAs of tile t + 1's scores are issued before tile t's softmax, so
   // they run while the softmax's VALU work issues, and the next tiles' operands are loaded a full
   // step before their use.  The last iteration recomputes its own tile's scores (unused) rather
   // than branch.
-  auto step = [&](int t, fa_f32x16& sv, fa_f32x16& snext) {
+  // vcur: this tile's V^T operands; vnext receives the next tile's (the two register sets
+  // alternate with the unrolled steps, so no operand is copied)
+  auto step = [&](int t, fa_f32x16& sv, fa_f32x16& snext, const uint4 (&vcur)[4],
+                  uint4 (&vnext)[4]) {
     snext = scores();
     // keys >= T exist only in the row's last tile
     const bool masked = t == ntiles - 1 && T % FA_KT != 0;
-    // this tile's V^T operands leave the load registers, which take the next tile's
-    const uint4 vcur[4] = {vr[0], vr[1], vr[2], vr[3]};
     load_k(min(t + 2, t1 - 1));
-    load_v(min(t + 1, t1 - 1));
-    if (masked) {
+    load_v(min(t + 1, t1 - 1), vnext);
+    if (__builtin_expect(masked, false)) {
 #pragma unroll
       for (int j = 0; j < 16; ++j)
-        if (t * FA_KT + 16 * (j >> 3) + 8 * hh + (j & 7) >= T) sv[j] = cpos ? -INFINITY : INFINITY;
+        if (t * FA_KT + 16 * (j >> 3) + 8 * hh + (j & 7) >= T) sv[j] = CPOS ? -INFINITY : INFINITY;
     }
     float mr;
-    if (cpos) {
+    if constexpr (CPOS) {
       mr = fmaxf(sv[0], sv[1]);
 #pragma unroll
       for (int j = 2; j < 16; j += 2) mr = fmaxf(mr, fmaxf(sv[j], sv[j + 1]));
@@ -219,7 +221,7 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint4* __restrict__ kp,
     // sv becomes the exponent s * c - m of each weight
 #pragma unroll
     for (int j = 0; j < 16; ++j) sv[j] = fmaf(sv[j], scale_log2, -m);
-    if (masked) {
+    if (__builtin_expect(masked, false)) {
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         if (t * FA_KT + 16 * (j >> 3) + 8 * hh + (j & 7) >= T) sv[j] = -INFINITY;
@@ -267,14 +269,15 @@ fa_bhwd_kernel(const uint16_t* __restrict__ q, const uint4* __restrict__ kp,
     }
   };
   if (t0 < t1) {
+    uint4 va[4], vb[4];
     load_k(t0);
-    load_v(t0);
+    load_v(t0, va);
     fa_f32x16 sa = scores(), sb;
     load_k(min(t0 + 1, t1 - 1));
-    // unrolled by two so that the two score buffers alternate without copies
+    // unrolled by two so that the two score buffers and the two V^T sets alternate without copies
     for (int t = t0; t < t1; t += 2) {
-      step(t, sa, sb);
-      if (t + 1 < t1) step(t + 1, sb, sa);
+      step(t, sa, sb, va, vb);
+      if (t + 1 < t1) step(t + 1, sb, sa, vb, va);
     }
   }
 
@@ -347,11 +350,18 @@ int mq_launch_flash_attn_bhwd(const void* q, const void* k, const void* v, void*
   hipLaunchKernelGGL(fa_pack_kernel, dim3(ntiles, bh), dim3(256), 0, stream, kk, vv, kp, vp, T,
                      ntiles);
   const dim3 grid((unsigned)(8 * per)), block(64 * FA_WAVES);
-  if (f16)
-    hipLaunchKernelGGL(fa_bhwd_kernel<true>, grid, block, 0, stream, qq, kp, vp, oo, T, scale_log2,
-                       nqb, (int)items, (int)per);
+  const bool cpos = scale_log2 >= 0.f;
+  if (f16 && cpos)
+    hipLaunchKernelGGL((fa_bhwd_kernel<true, true>), grid, block, 0, stream, qq, kp, vp, oo, T,
+                       scale_log2, nqb, (int)items, (int)per);
+  else if (f16)
+    hipLaunchKernelGGL((fa_bhwd_kernel<true, false>), grid, block, 0, stream, qq, kp, vp, oo, T,
+                       scale_log2, nqb, (int)items, (int)per);
+  else if (cpos)
+    hipLaunchKernelGGL((fa_bhwd_kernel<false, true>), grid, block, 0, stream, qq, kp, vp, oo, T,
+                       scale_log2, nqb, (int)items, (int)per);
   else
-    hipLaunchKernelGGL(fa_bhwd_kernel<false>, grid, block, 0, stream, qq, kp, vp, oo, T,
+    hipLaunchKernelGGL((fa_bhwd_kernel<false, false>), grid, block, 0, stream, qq, kp, vp, oo, T,
                        scale_log2, nqb, (int)items, (int)per);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
