@@ -1948,17 +1948,23 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, 
 //   q|k|v GEMM (input RMSNorm folded in) -> attention per (kv head, 16-query block): q/k RMSNorm,
 //   RoPE, K/V cache rows, causal softmax -> O GEMM + residual -> gate|up GEMM (post RMSNorm
 //   folded in) + silu(g) * u -> down GEMM + residual.
-// A GEMM stage gives a workgroup one tile of 16 output columns: its 16 weight rows are loaded
-// into registers before the barrier that precedes the stage, and all n rows of the fp32 input
-// are read with device-coherent loads after it.  Products run on v_mfma_f32_16x16x32_bf16 with
+// A GEMM stage's weight tiles (16 rows each) are loaded before the barrier that precedes the
+// stage, and its fp32 input rows with plain loads after it (every activation buffer of a launch is
+// written once and read only after the barrier that follows its writes).  The q|k|v and gate|up
+// stages give a workgroup one 16-row block and 1-4 column tiles (more as n grows, so that each
+// workgroup reads one block of input rows, staged straight into LDS); the O and down stages give
+// it one column tile and a quarter of the rows.  Products run on v_mfma_f32_16x16x32_bf16 with
 // the fp32 input split into three bf16 parts (hi + mid + lo represent it exactly), so each
 // product is the exact product of the fp32 value and the bf16 weight, accumulated in fp32.
 // The RMSNorm of a GEMM input is folded in: the MFMAs take x * w_norm and the epilogue scales
 // each row by rsqrt(mean(x^2) + eps), which the same pass accumulates.
 #define FP_STRIPES 32                    // barrier counter stripes, one 128-byte line each
 #define FPA_S 132                        // padded row stride (floats) of the attention tiles
-#define FP_LDS_FLOATS (160 * FPA_S + 32 * 64 + 64)
-static_assert(FP_LDS_FLOATS >= 2 * 8 * 4 * 256 + 8 * 64, "GEMM partials fit the attention carve");
+#define FP_IN_FLOATS (MQ_WAVES * (MQ_H / 256) * 2 * 256)   // the staged input block (K = H)
+#define FP_PART_FLOATS (8 * 4 * 256)                      // fp_gemm's partials
+#define FP_LDS_FLOATS (FP_PART_FLOATS + 16 * MQ_I / 2)       // + the down stage's tile (bf16)
+static_assert(FP_LDS_FLOATS >= 6 * 8 * 256 + 128 + FP_IN_FLOATS, "fp_gemm_rows16's carve fits");
+static_assert(FP_LDS_FLOATS >= 160 * FPA_S + 32 * 64 + 64, "the attention carve fits");
 static_assert(FP_LDS_FLOATS >= MQ_LDS_FLOATS, "the LM head's LDS layout fits");
 
 // Grid barrier over the launch: every thread's stores complete before the workgroup arrives at
@@ -2019,6 +2025,23 @@ MQ_DEV void fp_tile_load(FpTile<K>& t, const bf16_t* row0, bool shared = false) 
     t.b[j] = shared ? ld16(r + 32 * (wave + 8 * j)) : ld_nt16(r + 32 * (wave + 8 * j));
 }
 
+// The same tile held in LDS instead of registers, for a stage whose input needs the registers
+// (the down stage: 12 k-steps): wave w's operands at dst + (w (K / 256) + j) 64 + lane, where
+// fp_tile_load would put them in t.b[j], loaded straight into LDS (global_load_lds_dwordx4).
+// Counted by vmcnt like fp_tile_load's loads.
+template <int K>
+MQ_DEV void fp_tile_load_lds(uint4* dst, const bf16_t* row0) {
+  asm volatile("" ::: "memory");
+  const int lane = lane_id(), wave = wave_id();
+  const bf16_t* r = row0 + (size_t)(lane & 15) * K + 8 * (lane >> 4);
+  uint4* base = dst + __builtin_amdgcn_readfirstlane(wave) * (K / 256) * 64;
+#pragma unroll
+  for (int j = 0; j < K / 256; ++j)
+    __builtin_amdgcn_global_load_lds(
+        (const __attribute__((address_space(1))) void*)(r + 32 * (wave + 8 * j)),
+        (__attribute__((address_space(3))) void*)(base + j * 64), 16, 0, 0);
+}
+
 // x = hi + mid + lo exactly, each part bf16: v_cvt_pk_bf16_f32 rounds to nearest even, and each
 // remainder is exact in fp32 (the leading part takes the top 8 significant bits, the next the
 // following 8, the last the rest).
@@ -2043,23 +2066,21 @@ MQ_DEV void split3_bf16(const float (&x)[8], mq_bf16x8_t& hi, mq_bf16x8_t& mid, 
   lo = bf16x8_of(make_uint4(l[0], l[1], l[2], l[3]));
 }
 
-// One GEMM tile: C[r][c] = sum_k A[r][k] (* w_norm[k]) * W[c][k] for the rows r < n of 16-row
-// blocks rb0 .. rb0 + nbr - 1 (nbr <= 4) of the fp32 input A (row stride K; a buffer written
-// once per launch, read with plain loads) and the NT weight tiles, then
-// epi(row, col, v[NT], res) for every such row and the tile's 16 columns, where res = pre(row,
-// col) is loaded before the products (the residual of the O and down stages; 0 elsewhere), so
-// its round trip overlaps them.  With NORM the values are scaled by the row's
-// rsqrt(mean(A[r]^2) + eps) (the RMSNorm with weight w_norm).  All 512 threads take part.
-template <int K, bool NORM, int NT, class Pre, class Epi>
-MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, const bf16_t* w_norm,
-                    const FpTile<K> (&t)[NT], float* lds, Pre pre, Epi epi, int row_lo = 0) {
+// One residual GEMM tile (the O and down stages): C[r][c] = sum_k A[r][k] W[c][k] for the rows
+// row_lo <= r < n of 16-row blocks rb0 .. rb0 + nbr - 1 (nbr <= 4) of the fp32 input A (row
+// stride K; a buffer written once per launch, read with plain loads) and the 16 weight rows whose
+// k-step j operand of this lane is tb(j) (FpTile order), then epi(row, col, v, res) for every
+// such row and the tile's 16 columns, where res = pre(row, col) is loaded before the products
+// (the residual), so its round trip overlaps them.  All 512 threads take part.
+template <int K, class TB, class Pre, class Epi>
+MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, TB tb, float* lds, Pre pre, Epi epi,
+                    int row_lo) {
   // rows below row_lo are left to another workgroup (zero inputs, no outputs); block row i of
   // block b is row 16 (rb0 + b) + i
   const int lane = lane_id(), wave = wave_id();
-  // per-wave partials [NT][8 waves][4 blocks][16 rows][16 cols] and row sums [8][64]: C element
-  // i of lane l is (row 4 (l / 16) + i, column l % 16) of the block
+  // per-wave partials [8 waves][4 blocks][16 rows][16 cols]: C element i of lane l is
+  // (row 4 (l / 16) + i, column l % 16) of the block
   float* part = lds;
-  float* rs = lds + NT * 8 * 4 * 256;
   // this thread's epilogue elements (idx = tid + 512 k) and their residuals, loaded first
   float res[2];
 #pragma unroll
@@ -2068,80 +2089,51 @@ MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, const bf16_t* w_nor
     const int row = 16 * (rb0 + bl) + (e >> 4);
     res[k] = bl < nbr && row >= row_lo && row < n ? pre(row, e & 15) : 0.f;
   }
-  // the norm weights of this wave's k-steps (the same for every block)
-  uint4 wn16[NORM ? K / 256 : 1];
-  if constexpr (NORM) {
-#pragma unroll
-    for (int j = 0; j < K / 256; ++j) wn16[j] = ld16(w_norm + 32 * (wave + 8 * j) + 8 * (lane >> 4));
-  }
-  // 16-row blocks in batches of BB: all of a batch's input loads of this wave are issued before
-  // the first is used (one round trip per batch).
-  constexpr int BB = 1;
-  for (int b0 = 0; b0 < nbr; b0 += BB) {
-    // keeps the next batch's loads from being hoisted into this one (they would pin registers)
+  for (int bb = 0; bb < nbr; ++bb) {
+    // keeps the next block's loads from being hoisted into this one (they would pin registers)
     asm volatile("" ::: "memory");
-    uint64_t u[BB][K / 256][4];
+    static_assert(K % 1024 == 0, "k-steps in groups of four");
+    uint4 u[K / 256][2];
+    const int row = 16 * (rb0 + bb) + (lane & 15);
+    const bool in = row >= row_lo && row < n;
 #pragma unroll
-    for (int sb = 0; sb < BB; ++sb) {
-      const int row = 16 * (rb0 + b0 + sb) + (lane & 15);
-#pragma unroll
-      for (int j = 0; j < K / 256; ++j) {
-        const float* src = A + (size_t)row * K + 32 * (wave + 8 * j) + 8 * (lane >> 4);
-        const bool in = row >= row_lo && row < n;
-        const uint4 a = in ? ld16(src) : make_uint4(0, 0, 0, 0);
-        const uint4 b = in ? ld16(src + 4) : make_uint4(0, 0, 0, 0);
-        u[sb][j][0] = (uint64_t)a.x | ((uint64_t)a.y << 32);
-        u[sb][j][1] = (uint64_t)a.z | ((uint64_t)a.w << 32);
-        u[sb][j][2] = (uint64_t)b.x | ((uint64_t)b.y << 32);
-        u[sb][j][3] = (uint64_t)b.z | ((uint64_t)b.w << 32);
-      }
+    for (int j = 0; j < K / 256; ++j) {
+      const float* src = A + (size_t)row * K + 32 * (wave + 8 * j) + 8 * (lane >> 4);
+      u[j][0] = in ? ld16(src) : make_uint4(0, 0, 0, 0);
+      u[j][1] = in ? ld16(src + 4) : make_uint4(0, 0, 0, 0);
     }
+    // the weight operands are fetched four k-steps at a time (from LDS they would otherwise be
+    // read one k-step at a time, each read's latency in series with the products; all at once
+    // would take 48 more registers)
+    mq_f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int sb = 0; sb < BB; ++sb) {
-      const int bb = b0 + sb;
-      if (bb >= nbr) break;
-      mq_f32x4_t c[NT];
+    for (int j0 = 0; j0 < K / 256; j0 += 4) {
+      uint4 bt[4];
 #pragma unroll
-      for (int q = 0; q < NT; ++q) c[q] = mq_f32x4_t{0.f, 0.f, 0.f, 0.f};
-      float ss = 0.f;
+      for (int jj = 0; jj < 4; ++jj) {
+        const uint4 t = tb(j0 + jj);
+        mq_u32x4 v = {t.x, t.y, t.z, t.w};
+        asm volatile("" : "+v"(v));   // keeps the scheduler from sinking each read to its use
+        bt[jj] = make_uint4(v.x, v.y, v.z, v.w);
+      }
 #pragma unroll
-      for (int j = 0; j < K / 256; ++j) {
-        float x[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x[2 * i] = __uint_as_float((uint32_t)u[sb][j][i]);
-          x[2 * i + 1] = __uint_as_float((uint32_t)(u[sb][j][i] >> 32));
-        }
-        if constexpr (NORM) {
-          float wn[8];
-          unpack8(wn16[j], wn);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            ss = fmaf(x[e], x[e], ss);
-            x[e] *= wn[e];
-          }
-        }
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = j0 + jj;
+        const float x[8] = {__uint_as_float(u[j][0].x), __uint_as_float(u[j][0].y),
+                            __uint_as_float(u[j][0].z), __uint_as_float(u[j][0].w),
+                            __uint_as_float(u[j][1].x), __uint_as_float(u[j][1].y),
+                            __uint_as_float(u[j][1].z), __uint_as_float(u[j][1].w)};
         mq_bf16x8_t hi, mid, lo;
         split3_bf16(x, hi, mid, lo);
-#pragma unroll
-        for (int q = 0; q < NT; ++q) {
-          const mq_bf16x8_t b = bf16x8_of(t[q].b[j]);
-          c[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, c[q], 0, 0, 0);
-          c[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, c[q], 0, 0, 0);
-          c[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, c[q], 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < NT; ++q)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          part[((q * 8 + wave) * 4 + bb) * 256 + (4 * (lane >> 4) + i) * 16 + (lane & 15)] =
-              c[q][i];
-      if constexpr (NORM) {
-        const float sr = sum_xor32(sum_xor16(ss));   // the four lanes of row l % 16
-        if (lane < 16) rs[wave * 64 + 16 * bb + lane] = sr;
+        const mq_bf16x8_t b = bf16x8_of(bt[jj]);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, c, 0, 0, 0);
       }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      part[(wave * 4 + bb) * 256 + (4 * (lane >> 4) + i) * 16 + (lane & 15)] = c[i];
   }
   __syncthreads();
 #pragma unroll
@@ -2149,22 +2141,109 @@ MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, const bf16_t* w_nor
     const int idx = tid() + MQ_THREADS * k, bl = idx >> 8, e = idx & 255;
     const int row = 16 * (rb0 + bl) + (e >> 4), col = e & 15;
     if (bl >= nbr || row < row_lo || row >= n) continue;
-    float r = 1.f;
-    if constexpr (NORM) {
-      float s = 0.f;
+    float a = 0.f;
 #pragma unroll
-      for (int w8 = 0; w8 < 8; ++w8) s += rs[w8 * 64 + 16 * bl + (e >> 4)];
-      r = rsqrtf(s * (1.0f / K) + MQ_EPS);
+    for (int w8 = 0; w8 < 8; ++w8) a += part[(w8 * 4 + bl) * 256 + e];
+    epi(row, col, a, res[k]);
+  }
+  __syncthreads();
+}
+
+// One 16-row block of a normed GEMM stage over several column tiles: for the rows r < n of block
+// rb of the fp32 input A (row stride K), C_q[r][c] = rsqrt(mean(A[r]^2) + eps) *
+// sum_k A[r][k] w_norm[k] W_q[c][k] for the weight tiles q = g + NG s (g < ng, s < SUB) of t,
+// then epi(row, g, col, v[SUB]) for every such row, tile group g < ng and column col < 16, with
+// v[s] = C_{g + NG s} (SUB = 2: the gate and up tiles of one column range).  The block's input
+// rows are loaded once, in one round trip, straight into LDS (global_load_lds_dwordx4: each wave
+// stages its own k-steps, so they take no registers while in flight); all 512 threads take part,
+// and the sums run in the same order as fp_gemm's.
+template <int K, int NG, int SUB, class Epi>
+MQ_DEV void fp_gemm_rows16(const float* A, int n, int rb, const bf16_t* w_norm,
+                           const FpTile<K> (&t)[NG * SUB], int ng, float* lds, Epi epi) {
+  constexpr int NT = NG * SUB, KS = K / 256;
+  static_assert(MQ_WAVES * KS * 2 * 256 <= FP_IN_FLOATS, "the staged input fits");
+  const int lane = lane_id(), wave = wave_id();
+  // per-wave partials [NT][8 waves][16 rows][16 cols] (C element i of lane l is row
+  // 4 (l / 16) + i, column l % 16), the row sums of squares [8 waves][16 rows], then the staged
+  // input [8 waves][KS][2][64 lanes][4 floats]: lane l's floats 4 h .. 4 h + 3 of k-step j
+  float* part = lds;
+  float* rs = lds + NT * 8 * 256;
+  float* inp = rs + 128 + __builtin_amdgcn_readfirstlane(wave) * (KS * 2 * 256);
+  // rows past n load row n - 1 (written, in range) and are zeroed when converted
+  const int row = 16 * rb + (lane & 15);
+  const bool in = row < n;
+  const float* src = A + (size_t)min(row, n - 1) * K + 32 * wave + 8 * (lane >> 4);
+#pragma unroll
+  for (int j = 0; j < KS; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(src + 256 * j + 4 * h),
+          (__attribute__((address_space(3))) void*)(inp + (2 * j + h) * 256), 16, 0, 0);
+  uint4 wn16[KS];
+#pragma unroll
+  for (int j = 0; j < KS; ++j) wn16[j] = ld16(w_norm + 32 * (wave + 8 * j) + 8 * (lane >> 4));
+  mq_f32x4_t c[NT];
+#pragma unroll
+  for (int q = 0; q < NT; ++q) c[q] = mq_f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < KS; ++j) {
+    const float4 a0 = reinterpret_cast<const float4*>(inp + 2 * j * 256)[lane];
+    const float4 a1 = reinterpret_cast<const float4*>(inp + (2 * j + 1) * 256)[lane];
+    float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    if (!in)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    float wn[8];
+    unpack8(wn16[j], wn);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ss = fmaf(x[e], x[e], ss);
+      x[e] *= wn[e];
     }
-    float v[NT];
+    mq_bf16x8_t hi, mid, lo;
+    split3_bf16(x, hi, mid, lo);
 #pragma unroll
     for (int q = 0; q < NT; ++q) {
-      float a = 0.f;
-#pragma unroll
-      for (int w8 = 0; w8 < 8; ++w8) a += part[((q * 8 + w8) * 4 + bl) * 256 + e];
-      v[q] = NORM ? a * r : a;
+      if (q % NG >= ng) continue;
+      const mq_bf16x8_t b = bf16x8_of(t[q].b[j]);
+      c[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, c[q], 0, 0, 0);
+      c[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, c[q], 0, 0, 0);
+      c[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, c[q], 0, 0, 0);
     }
-    epi(row, col, v, res[k]);
+    // one k-step's split parts live at a time (hoisting them all would exceed the registers)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int q = 0; q < NT; ++q) {
+    if (q % NG >= ng) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      part[(q * 8 + wave) * 256 + (4 * (lane >> 4) + i) * 16 + (lane & 15)] = c[q][i];
+  }
+  const float sr = sum_xor32(sum_xor16(ss));   // the four lanes of row l % 16
+  if (lane < 16) rs[wave * 16 + lane] = sr;
+  __syncthreads();
+  constexpr int KE = (NG * 256 + MQ_THREADS - 1) / MQ_THREADS;
+#pragma unroll
+  for (int k = 0; k < KE; ++k) {
+    const int idx = tid() + MQ_THREADS * k, g = idx >> 8, e = idx & 255;
+    const int r16 = e >> 4, rw = 16 * rb + r16;
+    if (g >= ng || rw >= n) continue;
+    float s = 0.f;
+#pragma unroll
+    for (int w8 = 0; w8 < 8; ++w8) s += rs[w8 * 16 + r16];
+    const float r = rsqrtf(s * (1.0f / K) + MQ_EPS);
+    float v[SUB];
+#pragma unroll
+    for (int sb = 0; sb < SUB; ++sb) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w8 = 0; w8 < 8; ++w8) acc += part[((g + NG * sb) * 8 + w8) * 256 + e];
+      v[sb] = acc * r;
+    }
+    epi(rw, g, e & 15, v);
   }
   __syncthreads();
 }
@@ -2339,11 +2418,18 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
   const int hb_nb = hb_hi > hb_lo ? (hb_hi - 1) / 16 - hb_rb + 1 : 0;
   const bool hb_work = hb_lo < n;
   const bool hb_shared = n > hb_rows;
-  auto no_pre = [](int, int) { return 0.f; };
-  FpTile<MQ_H> tq[1];
-  const bool q_tile = wg < QKV / 16;
-  if (p.num_layers > 0 && q_tile) fp_tile_load(tq[0], qkv_row(p.layers[0], 16 * wg));
-  grid_sync(integral_constant<int, MQ_H / 256>(), p.num_layers > 0 && q_tile);
+  // The q|k|v and gate|up stages give a workgroup one 16-row block and qn (gp) column tiles of 16
+  // (gate|up: gp tiles of each), qn = 1, 2, 4, 4 and gp = 1, 2, 3, 3 for nb = 1 .. 4 row blocks:
+  // wg = block * groups + group, so the nb workgroups of a column group run on one XCD and share
+  // its weight tiles through the L2, and each reads one block of input rows, in one round trip.
+  const int qn = nb == 1 ? 1 : nb == 2 ? 2 : 4, gp = nb == 1 ? 1 : nb == 2 ? 2 : 3;
+  const int q_groups = QKV / 16 / qn, g_groups = MQ_I / 16 / gp;
+  const int q_grp = wg % q_groups, q_rb = wg / q_groups;
+  const int g_grp = wg % g_groups, g_rb = wg / g_groups;
+  const bool q_tile = q_rb < nb, g_tile = g_rb < nb;
+  // Each GEMM stage loads its weight tiles, then waits at the grid barrier (whose poll is issued
+  // behind them: the tiles stream in while it waits), then runs; the three sit in one branch so
+  // that the tiles' registers never cross a join (the register allocator spills them otherwise).
   for (int l = 0; l < p.num_layers; ++l) {
     const MqLayerW w = p.layers[l];
     const float* hin = hbuf(2 * l);
@@ -2353,54 +2439,90 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
     float* attl = attbuf(l);
     float* ml = mbuf(l);
     // q|k|v (prefill_mk_rmsnorm + prefill_mk_qkv_projection, :35-184)
-    if (wg < QKV / 16)
-      fp_gemm<MQ_H, true, 1>(hin, n, 0, nb, w.in_ln, tq, lds, no_pre,
-                             [&](int row, int col, const float* v, float) {
-        st_coh(qkvl + (size_t)row * QKV + 16 * wg + col, v[0]);
+    if (q_tile) {
+      FpTile<MQ_H> tq[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (q < qn) fp_tile_load(tq[q], qkv_row(w, 16 * (q_grp * qn + q)), nb > 1);
+      if (qn == 1)
+        grid_sync(integral_constant<int, MQ_H / 256>(), true);
+      else if (qn == 2)
+        grid_sync(integral_constant<int, 2 * MQ_H / 256>(), true);
+      else
+        grid_sync(integral_constant<int, 4 * MQ_H / 256>(), true);
+      fp_gemm_rows16<MQ_H, 4, 1>(hin, n, q_rb, w.in_ln, tq, qn, lds,
+                                 [&](int row, int g, int col, const float* v) {
+        st_coh(qkvl + (size_t)row * QKV + 16 * (q_grp * qn + g) + col, v[0]);
       });
+    } else {
+      grid_sync(integral_constant<int, 0>(), false);
+    }
     grid_sync(integral_constant<int, 0>(), false);
     if (wg < MQ_NKV * ((n + FP_QB - 1) / FP_QB))
       fp_attention(p, f, w, l, wg % MQ_NKV, wg / MQ_NKV, qkvl, attl, lds);
-    FpTile<MQ_QDIM> to[1];
-    if (hb_work) fp_tile_load(to[0], w.wo + (size_t)16 * hb_tile * MQ_QDIM, hb_shared);
-    grid_sync(integral_constant<int, MQ_QDIM / 256>(), hb_work);
     // O projection + residual (prefill_mk_o_proj_residual, :417-472)
-    if (hb_work)
-      fp_gemm<MQ_QDIM, false, 1>(attl, hb_hi, hb_rb, hb_nb, nullptr, to, lds,
-                                 [&](int row, int col) {
-                                   return *gptr<float>(hin + (size_t)row * MQ_H + 16 * hb_tile + col);
-                                 },
-                                 [&](int row, int col, const float* v, float res) {
-        st_coh(hmid + (size_t)row * MQ_H + 16 * hb_tile + col, res + v[0]);
+    if (hb_work) {
+      FpTile<MQ_QDIM> to;
+      fp_tile_load(to, w.wo + (size_t)16 * hb_tile * MQ_QDIM, hb_shared);
+      grid_sync(integral_constant<int, MQ_QDIM / 256>(), true);
+      fp_gemm<MQ_QDIM>(attl, hb_hi, hb_rb, hb_nb, [&](int j) { return to.b[j]; }, lds,
+                       [&](int row, int col) {
+                         return *gptr<float>(hin + (size_t)row * MQ_H + 16 * hb_tile + col);
+                       },
+                       [&](int row, int col, float v, float res) {
+        st_coh(hmid + (size_t)row * MQ_H + 16 * hb_tile + col, res + v);
       }, hb_lo);
-    FpTile<MQ_H> tgu[2];
-    if (wg < MQ_I / 16) {
-      fp_tile_load(tgu[0], w.wg + (size_t)16 * wg * MQ_H);
-      fp_tile_load(tgu[1], w.wu + (size_t)16 * wg * MQ_H);
+    } else {
+      grid_sync(integral_constant<int, 0>(), false);
     }
-    grid_sync(integral_constant<int, 2 * MQ_H / 256>(), wg < MQ_I / 16);
     // post RMSNorm + gate|up + silu(g) * u (prefill_mk_mlp_gate_up, :474-544)
-    if (wg < MQ_I / 16)
-      fp_gemm<MQ_H, true, 2>(hmid, n, 0, nb, w.post_ln, tgu, lds, no_pre,
-                             [&](int row, int col, const float* v, float) {
-        const float g = v[0], u = v[1];
-        st_coh(ml + (size_t)row * MQ_I + 16 * wg + col, g / (1.0f + expf(-g)) * u);
+    if (g_tile) {
+      // gate tiles in tgu[0 .. gp - 1], up tiles in tgu[3 .. 3 + gp - 1]
+      FpTile<MQ_H> tgu[6];
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+        if (q < gp) fp_tile_load(tgu[q], w.wg + (size_t)16 * (g_grp * gp + q) * MQ_H, nb > 1);
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+        if (q < gp) fp_tile_load(tgu[3 + q], w.wu + (size_t)16 * (g_grp * gp + q) * MQ_H, nb > 1);
+      if (gp == 1)
+        grid_sync(integral_constant<int, 2 * MQ_H / 256>(), true);
+      else if (gp == 2)
+        grid_sync(integral_constant<int, 4 * MQ_H / 256>(), true);
+      else
+        grid_sync(integral_constant<int, 6 * MQ_H / 256>(), true);
+      fp_gemm_rows16<MQ_H, 3, 2>(hmid, n, g_rb, w.post_ln, tgu, gp, lds,
+                                 [&](int row, int g, int col, const float* v) {
+        const float gt = v[0], u = v[1];
+        st_coh(ml + (size_t)row * MQ_I + 16 * (g_grp * gp + g) + col, gt / (1.0f + expf(-gt)) * u);
       });
-    FpTile<MQ_I> td[1];
-    if (hb_work) fp_tile_load(td[0], w.wd + (size_t)16 * hb_tile * MQ_I, hb_shared);
-    grid_sync(integral_constant<int, MQ_I / 256>(), hb_work);
+    } else {
+      grid_sync(integral_constant<int, 0>(), false);
+    }
     // down projection + residual (prefill_mk_mlp_down_residual, :546-599)
-    if (hb_work)
-      fp_gemm<MQ_I, false, 1>(ml, hb_hi, hb_rb, hb_nb, nullptr, td, lds,
-                              [&](int row, int col) {
-                                return *gptr<float>(hmid + (size_t)row * MQ_H + 16 * hb_tile + col);
-                              },
-                              [&](int row, int col, const float* v, float res) {
-        st_coh(hout + (size_t)row * MQ_H + 16 * hb_tile + col, res + v[0]);
+    if (hb_work) {
+      // the tile in LDS (the stage's input rows take 96 registers)
+      uint4* td = reinterpret_cast<uint4*>(lds + FP_PART_FLOATS);
+      fp_tile_load_lds<MQ_I>(td, w.wd + (size_t)16 * hb_tile * MQ_I);
+      grid_sync(integral_constant<int, MQ_I / 256>(), true);
+      // the tile has landed (its loads precede the barrier's poll); waiting here, before the
+      // input loads, lets the products start as the first input k-steps arrive instead of after
+      // the last (a read of LDS written by global_load_lds otherwise waits for every load)
+      wait_all_memory();
+      const uint4* tdw = td + wave_id() * (MQ_I / 256) * 64 + lane_id();
+      fp_gemm<MQ_I>(ml, hb_hi, hb_rb, hb_nb, [&](int j) { return tdw[j * 64]; }, lds,
+                    [&](int row, int col) {
+                      return *gptr<float>(hmid + (size_t)row * MQ_H + 16 * hb_tile + col);
+                    },
+                    [&](int row, int col, float v, float res) {
+        st_coh(hout + (size_t)row * MQ_H + 16 * hb_tile + col, res + v);
       }, hb_lo);
-    if (l + 1 < p.num_layers && q_tile) fp_tile_load(tq[0], qkv_row(p.layers[l + 1], 16 * wg));
-    grid_sync(integral_constant<int, MQ_H / 256>(), l + 1 < p.num_layers && q_tile);
+    } else {
+      grid_sync(integral_constant<int, 0>(), false);
+    }
   }
+  // the last layer's residual stream (or the embeddings) is complete
+  grid_sync(integral_constant<int, 0>(), false);
   // final RMSNorm of the last position (fp32, prefill_mk_final_norm, :601-650) + LM head argmax
   const float2 hv = ldf2(hbuf(2 * p.num_layers) + (size_t)(n - 1) * MQ_H + 2 * t);
   lds[LDS_IN + 2 * t] = hv.x;
