@@ -2006,6 +2006,45 @@ MQ_DEV void fp_grid_sync(uint32_t* bar, uint32_t target, MqSync* sy) {
   __syncthreads();
 }
 
+// The launch's synchronization area (zeroed by the launcher): the grid barrier's 32 counter
+// stripes, then one role-claim counter per XCD, then per XCD one 128-byte line of flag words
+// (one per workgroup of the XCD) for the XCD-local barrier.
+#define FP_SYNC_WORDS ((FP_STRIPES + 2 * MQ_GROUPS) * 32)
+MQ_DEV uint32_t* fp_claims(uint32_t* bar) { return bar + FP_STRIPES * 32; }
+MQ_DEV uint32_t* fp_xflags(uint32_t* bar, int x) { return bar + (FP_STRIPES + MQ_GROUPS + x) * 32; }
+
+// Barrier of the workgroups of one XCD: each posts `e` in its flag word with a plain store (it
+// lands in the XCD's L2, where the others' sc1 loads find it) once its stores have completed,
+// and wave 0 polls the XCD's nw (<= 32) flags until every one is >= e (flags only grow within a
+// launch).  The error flag (every 16th round) or the spin bound ends the wait early, as in
+// fp_grid_sync.
+MQ_DEV void fp_xcd_sync(uint32_t* flags, int c, int nw, uint32_t e, MqSync* sy) {
+  wait_all_memory();
+  __syncthreads();
+  if (wave_id() == 0) {
+    const int lane = lane_id();
+    if (lane == 0) st_local32(flags + c, e);
+    uint32_t spins = 0;
+    while (true) {
+      const uint32_t v = lane < nw ? __hip_atomic_load(flags + lane, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                                   : e;
+      if (__all(v >= e)) break;
+      uint32_t ev = 0;
+      if (lane == 0 && (spins & 15) == 15)
+        ev = __hip_atomic_load(&sy->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_amdgcn_readlane(ev, 0) != 0) break;
+      if (++spins > MQ_SPIN_LIMIT) {
+        if (lane == 0)
+          __hip_atomic_store(&sy->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+}
+
 // 16 weight rows (row0 .. row0 + 15, K bf16 each) as the B operand of the tile's MFMAs: wave w
 // holds the 32-wide k-steps w, w + 8, ...; lane l holds row l % 16, k-dims 8 (l / 16) .. + 8.
 template <int K>
@@ -2372,8 +2411,27 @@ MQ_DEV void fp_attention(const MqDecodeParams& p, const MqFusedArgs& f, const Mq
 __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodeParams p,
                                                                       MqFusedArgs f) {
   __shared__ __align__(16) float lds[FP_LDS_FLOATS];
-  const int wg = blockIdx.x, G = gridDim.x, n = f.n, t = tid();
+  const int G = gridDim.x, n = f.n, t = tid();
   MqSync* sy = &p.st->sync;
+  // Role from the hardware placement, as the persistent decode kernel claims it: xc is the XCD
+  // the workgroup runs on and xj the order of its claim there; the role index wg = xc + 8 xj
+  // replaces the launch index everywhere, so wg % 8 is the XCD (the L2-shared tiles and the
+  // XCD-local q|k|v exchange rely on it).  A placement with more than G / 8 workgroups on one
+  // XCD flags error 4; that workgroup returns and the others' waits end on the error flag.
+  __shared__ int s_role;
+  if (t == 0) {
+    const uint32_t x = (uint32_t)xcc_id() & (MQ_GROUPS - 1);
+    s_role = (int)(x + MQ_GROUPS * __hip_atomic_fetch_add(fp_claims(f.bar) + x, 1u,
+                                                          __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT));
+  }
+  __syncthreads();
+  const int wg = __builtin_amdgcn_readfirstlane(s_role);
+  const int xc = wg % MQ_GROUPS, xj = wg / MQ_GROUPS, NX = G / MQ_GROUPS;
+  if (xj >= NX) {
+    if (t == 0) __hip_atomic_store(&sy->err.v, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   uint32_t nbar = 0;
   // LOADS: the weight-tile loads issued since the stage's last store, when `loaded`
   auto grid_sync = [&](auto loads, bool loaded) {
@@ -2419,12 +2477,20 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
   const bool hb_work = hb_lo < n;
   const bool hb_shared = n > hb_rows;
   // The q|k|v and gate|up stages give a workgroup one 16-row block and qn (gp) column tiles of 16
-  // (gate|up: gp tiles of each), qn = 1, 2, 4, 4 and gp = 1, 2, 3, 3 for nb = 1 .. 4 row blocks:
-  // wg = block * groups + group, so the nb workgroups of a column group run on one XCD and share
-  // its weight tiles through the L2, and each reads one block of input rows, in one round trip.
+  // (gate|up: gp tiles of each), qn = 1, 2, 4, 4 and gp = 1, 2, 3, 3 for nb = 1 .. 4 row blocks,
+  // and each reads one block of input rows, in one round trip.
+  // q|k|v: XCD x computes the 32 tiles of kv head x (q heads 2x, 2x + 1, then k and v of x;
+  // tile i of the head is qkv_tile(i)), so that its attention reads them from its own L2 after
+  // an XCD-local barrier: member xj takes block xj / (32 / qn) and tiles qn (xj % (32 / qn)) + q.
+  // gate|up: wg = block * groups + group, so the nb workgroups of a column group run on one XCD
+  // and share its weight tiles through the L2.
   const int qn = nb == 1 ? 1 : nb == 2 ? 2 : 4, gp = nb == 1 ? 1 : nb == 2 ? 2 : 3;
-  const int q_groups = QKV / 16 / qn, g_groups = MQ_I / 16 / gp;
-  const int q_grp = wg % q_groups, q_rb = wg / q_groups;
+  const int g_groups = MQ_I / 16 / gp;
+  const int q_grp = xj % (32 / qn), q_rb = xj / (32 / qn);
+  // tile i < 32 of kv head x: its 16-column index in q|k|v
+  auto qkv_tile = [](int x, int i) {
+    return i < 16 ? 16 * x + i : i < 24 ? 128 + 8 * x + (i - 16) : 192 + 8 * x + (i - 24);
+  };
   const int g_grp = wg % g_groups, g_rb = wg / g_groups;
   const bool q_tile = q_rb < nb, g_tile = g_rb < nb;
   // Each GEMM stage loads its weight tiles, then waits at the grid barrier (whose poll is issued
@@ -2440,26 +2506,31 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
     float* ml = mbuf(l);
     // q|k|v (prefill_mk_rmsnorm + prefill_mk_qkv_projection, :35-184)
     if (q_tile) {
+      // (the head index passes through an empty asm so that the tile addresses are recomputed
+      // here, not kept in registers across the layer loop)
+      int hx = xc;
+      asm volatile("" : "+s"(hx));
       FpTile<MQ_H> tq[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        if (q < qn) fp_tile_load(tq[q], qkv_row(w, 16 * (q_grp * qn + q)), nb > 1);
+        if (q < qn) fp_tile_load(tq[q], qkv_row(w, 16 * qkv_tile(hx, q_grp * qn + q)), nb > 1);
       if (qn == 1)
         grid_sync(integral_constant<int, MQ_H / 256>(), true);
       else if (qn == 2)
         grid_sync(integral_constant<int, 2 * MQ_H / 256>(), true);
       else
         grid_sync(integral_constant<int, 4 * MQ_H / 256>(), true);
+      // (plain stores: only this XCD reads them)
       fp_gemm_rows16<MQ_H, 4, 1>(hin, n, q_rb, w.in_ln, tq, qn, lds,
                                  [&](int row, int g, int col, const float* v) {
-        st_coh(qkvl + (size_t)row * QKV + 16 * (q_grp * qn + g) + col, v[0]);
+        qkvl[(size_t)row * QKV + 16 * qkv_tile(hx, q_grp * qn + g) + col] = v[0];
       });
     } else {
       grid_sync(integral_constant<int, 0>(), false);
     }
-    grid_sync(integral_constant<int, 0>(), false);
-    if (wg < MQ_NKV * ((n + FP_QB - 1) / FP_QB))
-      fp_attention(p, f, w, l, wg % MQ_NKV, wg / MQ_NKV, qkvl, attl, lds);
+    // q|k|v -> attention inside each XCD; attention item (kv head xc, query block xj)
+    fp_xcd_sync(fp_xflags(f.bar, xc), xj, NX, (uint32_t)(l + 1), sy);
+    if (xj < (n + FP_QB - 1) / FP_QB) fp_attention(p, f, w, l, xc, xj, qkvl, attl, lds);
     // O projection + residual (prefill_mk_o_proj_residual, :417-472)
     if (hb_work) {
       FpTile<MQ_QDIM> to;
@@ -2600,7 +2671,7 @@ size_t mq_fused_workspace_bytes(int num_layers) {
   const size_t L = (size_t)(num_layers > 0 ? num_layers : 0);
   return (size_t)MQ_FUSED_MAX_N * 4 *
              ((2 * L + 1) * MQ_H + L * (MQ_QDIM + 2 * MQ_KVDIM + MQ_QDIM + MQ_I)) +
-         FP_STRIPES * 128;
+         FP_SYNC_WORDS * 4;
 }
 void mq_fused_bind(MqFusedArgs* f, char* base, int num_layers) {
   const size_t L = (size_t)(num_layers > 0 ? num_layers : 0);
@@ -2626,7 +2697,8 @@ int mq_launch_prefill_fused(const MqDecodeParams& p, const MqFusedArgs& f, int g
   if (!g_coop_ok || g_fused_blocks_per_cu < 1 || grid > g_cu_count * g_fused_blocks_per_cu)
     return -2;
   if (grid < 256 || f.n < 1 || f.n > MQ_FUSED_MAX_N) return -3;
-  const int rc = mq_launch_zero(f.bar, FP_STRIPES * 128, stream);
+  if (grid / MQ_GROUPS > 32) return -3;   // fp_xcd_sync polls at most 32 flags per XCD
+  const int rc = mq_launch_zero(f.bar, FP_SYNC_WORDS * 4, stream);
   if (rc != 0) return rc;
   MqDecodeParams pc = p;
   MqFusedArgs fc = f;
