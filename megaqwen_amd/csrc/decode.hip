@@ -1964,7 +1964,9 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, 
 #define FP_PART_FLOATS (8 * 4 * 256)                      // fp_gemm's partials
 #define FP_LDS_FLOATS (FP_PART_FLOATS + 16 * MQ_I / 2)       // + the down stage's tile (bf16)
 static_assert(FP_LDS_FLOATS >= 6 * 8 * 256 + 128 + FP_IN_FLOATS, "fp_gemm_rows16's carve fits");
-static_assert(FP_LDS_FLOATS >= 160 * FPA_S + 32 * 64 + 64, "the attention carve fits");
+#define FPA_KS 136                       // bf16 row stride of the attention's split q / k planes
+static_assert(FP_LDS_FLOATS >= 3 * 72 * FPA_KS / 2 + 64 * FPA_S + 2 * 8 * 64,
+              "the attention carve fits");
 static_assert(FP_LDS_FLOATS >= MQ_LDS_FLOATS, "the LM head's LDS layout fits");
 
 // Grid barrier over the launch: every thread's stores complete before the workgroup arrives at
@@ -2086,20 +2088,21 @@ MQ_DEV void fp_tile_load_lds(uint4* dst, const bf16_t* row0) {
 // following 8, the last the rest).
 typedef float mq_f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 mq_bf16x2_t __attribute__((ext_vector_type(2)));
+MQ_DEV void split3_pair(float x0, float x1, uint32_t& h, uint32_t& m, uint32_t& l) {
+  const mq_f32x2_t v = {x0, x1};
+  const mq_bf16x2_t a = __builtin_convertvector(v, mq_bf16x2_t);
+  const mq_f32x2_t r = v - __builtin_convertvector(a, mq_f32x2_t);
+  const mq_bf16x2_t b = __builtin_convertvector(r, mq_bf16x2_t);
+  const mq_bf16x2_t c = __builtin_convertvector(r - __builtin_convertvector(b, mq_f32x2_t),
+                                                mq_bf16x2_t);
+  h = __builtin_bit_cast(uint32_t, a);
+  m = __builtin_bit_cast(uint32_t, b);
+  l = __builtin_bit_cast(uint32_t, c);
+}
 MQ_DEV void split3_bf16(const float (&x)[8], mq_bf16x8_t& hi, mq_bf16x8_t& mid, mq_bf16x8_t& lo) {
   uint32_t h[4], m[4], l[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const mq_f32x2_t v = {x[2 * i], x[2 * i + 1]};
-    const mq_bf16x2_t a = __builtin_convertvector(v, mq_bf16x2_t);
-    const mq_f32x2_t r = v - __builtin_convertvector(a, mq_f32x2_t);
-    const mq_bf16x2_t b = __builtin_convertvector(r, mq_bf16x2_t);
-    const mq_bf16x2_t c = __builtin_convertvector(r - __builtin_convertvector(b, mq_f32x2_t),
-                                                  mq_bf16x2_t);
-    h[i] = __builtin_bit_cast(uint32_t, a);
-    m[i] = __builtin_bit_cast(uint32_t, b);
-    l[i] = __builtin_bit_cast(uint32_t, c);
-  }
+  for (int i = 0; i < 4; ++i) split3_pair(x[2 * i], x[2 * i + 1], h[i], m[i], l[i]);
   hi = bf16x8_of(make_uint4(h[0], h[1], h[2], h[3]));
   mid = bf16x8_of(make_uint4(m[0], m[1], m[2], m[3]));
   lo = bf16x8_of(make_uint4(l[0], l[1], l[2], l[3]));
@@ -2302,6 +2305,25 @@ MQ_DEV float2 fp_norm_rope(float2 x, uint32_t w2, uint32_t c2, uint32_t s2) {
     return make_float2(n0 * bf16_lo(c2) - p0 * bf16_lo(s2), n1 * bf16_hi(c2) - p1 * bf16_hi(s2));
   return make_float2(p0 * bf16_lo(s2) + n0 * bf16_lo(c2), p1 * bf16_hi(s2) + n1 * bf16_hi(c2));
 }
+// The same for two rows at once, 4 dims per lane: lanes 0-31 hold one row and lanes 32-63 the
+// other, lane l dims 4 (l % 32) .. + 3 (weights w4, table entries c4, s4 of those dims); the
+// RMSNorm sums over the lane's half and the partner dims sit in lane l ^ 16.
+MQ_DEV float4 fp_norm_rope4(float4 x, uint2 w4, uint2 c4, uint2 s4) {
+  const int lane = lane_id();
+  const float sc = rsqrtf(sum_xor16(row16_sum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w)) *
+                              (1.0f / MQ_D) + MQ_EPS);
+  const float n0 = x.x * sc * bf16_lo(w4.x), n1 = x.y * sc * bf16_hi(w4.x);
+  const float n2 = x.z * sc * bf16_lo(w4.y), n3 = x.w * sc * bf16_hi(w4.y);
+  const bool lo = (lane & 16) == 0;              // dims < 64; the partner is lane ^ 16
+  const float2 s0 = swap16(n0), s1 = swap16(n1), s2 = swap16(n2), s3 = swap16(n3);
+  const float p0 = lo ? s0.y : s0.x, p1 = lo ? s1.y : s1.x;
+  const float p2 = lo ? s2.y : s2.x, p3 = lo ? s3.y : s3.x;
+  if (lo)
+    return make_float4(n0 * bf16_lo(c4.x) - p0 * bf16_lo(s4.x), n1 * bf16_hi(c4.x) - p1 * bf16_hi(s4.x),
+                       n2 * bf16_lo(c4.y) - p2 * bf16_lo(s4.y), n3 * bf16_hi(c4.y) - p3 * bf16_hi(s4.y));
+  return make_float4(p0 * bf16_lo(s4.x) + n0 * bf16_lo(c4.x), p1 * bf16_hi(s4.x) + n1 * bf16_hi(c4.x),
+                     p2 * bf16_lo(s4.y) + n2 * bf16_lo(c4.y), p3 * bf16_hi(s4.y) + n3 * bf16_hi(c4.y));
+}
 
 // Attention item (kv head h, query block qb = positions FP_QB qb .. FP_QB qb + FP_QB - 1) of
 // layer `layer` (prefill_mk_causal_attention, fused_prefill_megakernel_core.inl:328-414): both
@@ -2316,36 +2338,55 @@ MQ_DEV float2 ldf2(const float* p) {
   const uint64_t u = *gptr<uint64_t>(p);
   return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
 }
+MQ_DEV uint2 ld8(const void* p) {
+  const uint64_t u = *gptr<uint64_t>(p);
+  return make_uint2((uint32_t)u, (uint32_t)(u >> 32));
+}
+MQ_DEV float4 ldf4(const float* p) {
+  const uint4 u = ld16(p);
+  return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                     __uint_as_float(u.w));
+}
 MQ_DEV void fp_attention(const MqDecodeParams& p, const MqFusedArgs& f, const MqLayerW& w,
                          int layer, int h, int qb, const float* qkv, float* att, float* lds) {
   static_assert(2 * FP_QB == MQ_WAVES, "one query row per wave");
   static_assert(MQ_FUSED_MAX_N <= 64, "one key per lane");
-  float* Ks = lds;                       // [64][FPA_S] keys after norm + RoPE
-  float* Vs = lds + 64 * FPA_S;          // [64][FPA_S] values
-  float* Qs = lds + 128 * FPA_S;         // [8][FPA_S] query rows after norm + RoPE
-  float* Ps = lds + 136 * FPA_S;         // [8][64] softmax weights
+  // keys and query rows after norm + RoPE as three bf16 planes (hi, mid, lo: exact parts of the
+  // fp32 values), the A / B operands of the score MFMAs
+  bf16_t* Kp = reinterpret_cast<bf16_t*>(lds);  // [3][64][FPA_KS]
+  bf16_t* Qp = Kp + 3 * 64 * FPA_KS;            // [3][8][FPA_KS]
+  float* Vs = lds + 3 * 72 * FPA_KS / 2;        // [64][FPA_S] values
+  float* Ss = Vs + 64 * FPA_S;                  // [8][64] scores
+  float* Ps = Ss + 8 * 64;                      // [8][64] softmax weights
   const int n = f.n, q0 = FP_QB * qb, kn = min(n, q0 + FP_QB), qn = kn - q0;
   const int lane = lane_id(), wave = wave_id();
   constexpr int QKV = MQ_QDIM + 2 * MQ_KVDIM;
-  const uint32_t kw = ld32(w.k_norm + 2 * lane), qw = ld32(w.q_norm + 2 * lane);
+  const int half = lane >> 5, m4 = 4 * (lane & 31);
+  const uint2 kw = ld8(w.k_norm + m4);
+  const uint32_t qw = ld32(w.q_norm + 2 * lane);
   bf16_t* kc = p.kc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
   bf16_t* vc = p.vc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
-  // key rows j = wave + 8 i and this wave's query row: every load of the wave (raw rows and
-  // their RoPE table pairs) is issued before the first is used, one round trip in all
-  constexpr int KI = MQ_FUSED_MAX_N / MQ_WAVES;
-  float2 kr[KI], vr[KI], qr = make_float2(0.f, 0.f);
-  uint32_t kc2[KI], ks2[KI], qc2 = 0, qs2 = 0;
+  // key rows in pairs, lanes 0-31 row j0 = wave + 16 i and lanes 32-63 row j0 + 8 (4 dims per
+  // lane, so a 16-byte load moves two rows), and this wave's query row: every load of the wave
+  // (raw rows and their RoPE table entries) is issued before the first is used, one round trip
+  // in all.  The second row of a pair past the keys loads row kn - 1 and is not stored.
+  constexpr int KI = MQ_FUSED_MAX_N / (2 * MQ_WAVES);
+  float4 kr[KI], vr[KI];
+  uint2 kc4[KI], ks4[KI];
+  float2 qr = make_float2(0.f, 0.f);
+  uint32_t qc2 = 0, qs2 = 0;
   const int r = wave, pi = q0 + (r >> 1);        // this wave's query row and its position
   const bool has_q = r < 2 * qn;
 #pragma unroll
   for (int i = 0; i < KI; ++i) {
-    const int j = wave + MQ_WAVES * i;
-    if (j < kn) {
+    const int j0 = wave + 2 * MQ_WAVES * i;
+    if (j0 < kn) {
+      const int j = min(j0 + MQ_WAVES * half, kn - 1);
       const float* row = qkv + (size_t)j * QKV;
-      kr[i] = ldf2(row + MQ_QDIM + h * MQ_D + 2 * lane);
-      vr[i] = ldf2(row + MQ_QDIM + MQ_KVDIM + h * MQ_D + 2 * lane);
-      kc2[i] = ld32(p.cos + (size_t)j * MQ_D + 2 * lane);
-      ks2[i] = ld32(p.sin + (size_t)j * MQ_D + 2 * lane);
+      kr[i] = ldf4(row + MQ_QDIM + h * MQ_D + m4);
+      vr[i] = ldf4(row + MQ_QDIM + MQ_KVDIM + h * MQ_D + m4);
+      kc4[i] = ld8(p.cos + (size_t)j * MQ_D + m4);
+      ks4[i] = ld8(p.sin + (size_t)j * MQ_D + m4);
     }
   }
   if (has_q) {
@@ -2355,39 +2396,78 @@ MQ_DEV void fp_attention(const MqDecodeParams& p, const MqFusedArgs& f, const Mq
   }
 #pragma unroll
   for (int i = 0; i < KI; ++i) {
-    const int j = wave + MQ_WAVES * i;
-    if (j < kn) {
-      const float2 k = fp_norm_rope(kr[i], kw, kc2[i], ks2[i]);
-      reinterpret_cast<float2*>(Ks + j * FPA_S)[lane] = k;
-      reinterpret_cast<float2*>(Vs + j * FPA_S)[lane] = vr[i];
-      if (j >= q0) {
-        reinterpret_cast<uint32_t*>(kc + (size_t)j * MQ_D)[lane] =
-            (uint32_t)f32_to_bf16(k.x) | ((uint32_t)f32_to_bf16(k.y) << 16);
-        reinterpret_cast<uint32_t*>(vc + (size_t)j * MQ_D)[lane] =
-            (uint32_t)f32_to_bf16(vr[i].x) | ((uint32_t)f32_to_bf16(vr[i].y) << 16);
+    const int j0 = wave + 2 * MQ_WAVES * i;
+    if (j0 < kn) {
+      const int j = j0 + MQ_WAVES * half;
+      const float4 k = fp_norm_rope4(kr[i], kw, kc4[i], ks4[i]);
+      if (j < kn) {
+        uint32_t hw[2], mw[2], lw[2];
+        split3_pair(k.x, k.y, hw[0], mw[0], lw[0]);
+        split3_pair(k.z, k.w, hw[1], mw[1], lw[1]);
+        *reinterpret_cast<uint2*>(Kp + j * FPA_KS + m4) = make_uint2(hw[0], hw[1]);
+        *reinterpret_cast<uint2*>(Kp + (64 + j) * FPA_KS + m4) = make_uint2(mw[0], mw[1]);
+        *reinterpret_cast<uint2*>(Kp + (128 + j) * FPA_KS + m4) = make_uint2(lw[0], lw[1]);
+        *reinterpret_cast<float4*>(Vs + j * FPA_S + m4) = vr[i];
+        if (j >= q0) {
+          *reinterpret_cast<uint2*>(kc + (size_t)j * MQ_D + m4) =
+              make_uint2((uint32_t)f32_to_bf16(k.x) | ((uint32_t)f32_to_bf16(k.y) << 16),
+                         (uint32_t)f32_to_bf16(k.z) | ((uint32_t)f32_to_bf16(k.w) << 16));
+          *reinterpret_cast<uint2*>(vc + (size_t)j * MQ_D + m4) =
+              make_uint2((uint32_t)f32_to_bf16(vr[i].x) | ((uint32_t)f32_to_bf16(vr[i].y) << 16),
+                         (uint32_t)f32_to_bf16(vr[i].z) | ((uint32_t)f32_to_bf16(vr[i].w) << 16));
+        }
       }
     }
   }
-  if (has_q) reinterpret_cast<float2*>(Qs + r * FPA_S)[lane] = fp_norm_rope(qr, qw, qc2, qs2);
+  {
+    // this wave's query row (zeros for a wave without one)
+    uint32_t hq = 0, mq = 0, lq = 0;
+    if (has_q) {
+      const float2 q = fp_norm_rope(qr, qw, qc2, qs2);
+      split3_pair(q.x, q.y, hq, mq, lq);
+    }
+    reinterpret_cast<uint32_t*>(Qp + r * FPA_KS)[lane] = hq;
+    reinterpret_cast<uint32_t*>(Qp + (8 + r) * FPA_KS)[lane] = mq;
+    reinterpret_cast<uint32_t*>(Qp + (16 + r) * FPA_KS)[lane] = lq;
+  }
+  __syncthreads();
+  // Scores S = Q K^T on v_mfma_f32_16x16x32_bf16, wave w taking keys 16 w .. 16 w + 15: A rows
+  // are the 8 query rows (rows 8-15 zero), B columns the keys.  The six products of the parts
+  // down to hi * lo and mid * mid (smallest first) make each q k product exact to ~2^-23
+  // relative (the dropped mid * lo, lo * mid and lo * lo terms), accumulated in fp32.
+  if (wave < (kn + 15) / 16) {
+    const int col = lane & 15, kd = 8 * (lane >> 4);
+    const mq_bf16x8_t zero = bf16x8_of(make_uint4(0u, 0u, 0u, 0u));
+    mq_f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < MQ_D / 32; ++ks) {
+      mq_bf16x8_t a[3], b[3];
+#pragma unroll
+      for (int e = 0; e < 3; ++e) {
+        b[e] = bf16x8_of(*reinterpret_cast<const uint4*>(
+            Kp + (64 * e + 16 * wave + col) * FPA_KS + 32 * ks + kd));
+        a[e] = col < 8 ? bf16x8_of(*reinterpret_cast<const uint4*>(
+                             Qp + (8 * e + col) * FPA_KS + 32 * ks + kd))
+                       : zero;
+      }
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], c, 0, 0, 0);
+    }
+    // C element i of lane l: query row 4 (l / 16) + i, key 16 w + l % 16
+    if (lane < 32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Ss[(4 * (lane >> 4) + i) * 64 + 16 * wave + col] = c[i];
+    }
+  }
   __syncthreads();
   if (has_q) {
     // scores of keys j = lane <= pi (causal), the reference's scale
     const int j = lane;
-    float s = -INFINITY;
-    if (j < kn && j <= pi) {
-      float acc = 0.f;
-      const float4* qv = reinterpret_cast<const float4*>(Qs + r * FPA_S);
-      const float4* kv = reinterpret_cast<const float4*>(Ks + j * FPA_S);
-#pragma unroll 8
-      for (int d4 = 0; d4 < MQ_D / 4; ++d4) {
-        const float4 a = qv[d4], b = kv[d4];
-        acc = fmaf(a.x, b.x, acc);
-        acc = fmaf(a.y, b.y, acc);
-        acc = fmaf(a.z, b.z, acc);
-        acc = fmaf(a.w, b.w, acc);
-      }
-      s = acc * rsqrtf((float)MQ_D);
-    }
+    const float s = j < kn && j <= pi ? Ss[r * 64 + j] * rsqrtf((float)MQ_D) : -INFINITY;
     const float mx = wave_max(s);
     const float e = s == -INFINITY ? 0.f : expf(s - mx);
     const float inv = 1.0f / wave_sum(e);
