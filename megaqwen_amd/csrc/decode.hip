@@ -2330,9 +2330,10 @@ MQ_DEV float4 fp_norm_rope4(float4 x, uint2 w4, uint2 c4, uint2 s4) {
 // query heads 2h, 2h + 1 of the block against keys 0 .. min(n, FP_QB (qb + 1)) - 1, fp32
 // throughout (the keys normalised and rotated here from the raw q|k|v rows; the block's own
 // positions' K/V rows are also written to the bf16 cache).  Scores use the reference's scale and
-// an expf softmax.  Wave r holds query row r (position q0 + r / 2, head 2h + r % 2): lane j
-// scores key j (the q row is an LDS broadcast), the softmax is a wave reduction, and in P.V
-// lane l accumulates dims 2l, 2l + 1 over the keys in order.
+// an expf softmax.  The q k^T products run on MFMA from exact three-part bf16 splits of the fp32
+// rows (below); then wave r holds query row r (position q0 + r / 2, head 2h + r % 2): lane j
+// takes key j's score, the softmax is a wave reduction, and in P.V lane l accumulates dims
+// 2l, 2l + 1 over the keys in order.
 #define FP_QB 4
 MQ_DEV float2 ldf2(const float* p) {
   const uint64_t u = *gptr<uint64_t>(p);
