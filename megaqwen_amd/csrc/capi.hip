@@ -112,8 +112,18 @@ struct mq_decoder {
   char* ws;
   MqPrefillBuffers pf;
   MqFusedArgs fused;
+  // tag of the last fused-prefill launch that wrote each row of the tagged activation buffers
+  // (0: zeros since creation or reset)
+  uint8_t fused_tag[MQ_FUSED_MAX_N];
   std::vector<MqLayerW> host_layers;
 };
+
+// Zeroes the fused prefill's tagged activation buffers and forgets their tags.
+static int clear_fused_tags(mq_decoder* dec, hipStream_t s) {
+  memset(dec->fused_tag, 0, sizeof(dec->fused_tag));
+  if (dec->max_prefill <= 0) return 0;
+  return mq_launch_zero(dec->fused.h, mq_fused_activation_bytes(dec->p.num_layers), s);
+}
 
 extern "C" {
 
@@ -227,7 +237,7 @@ int mq_decoder_create(const mq_model_desc* desc, void* k_cache, void* v_cache, v
   mq_prefill_bind(&dec->pf, ws + lay.prefill, desc->max_prefill_len);
   memset(&dec->fused, 0, sizeof(dec->fused));
   if (desc->max_prefill_len > 0) mq_fused_bind(&dec->fused, ws + lay.fused, desc->num_layers);
-  if (mq_launch_clear_state(p.st, p.x, nullptr) != 0 ||
+  if (mq_launch_clear_state(p.st, p.x, nullptr) != 0 || clear_fused_tags(dec, nullptr) != 0 ||
       (dec->pf.cnt != nullptr && mq_launch_zero(dec->pf.cnt, dec->pf.cnt_bytes, nullptr) != 0) ||
       hipStreamSynchronize(nullptr) != hipSuccess) {
     delete dec;
@@ -247,7 +257,7 @@ int mq_decoder_reset(mq_decoder* dec, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (mq_launch_zero(dec->p.kc, dec->kv_bytes, s) != 0 ||
       mq_launch_zero(dec->p.vc, dec->kv_bytes, s) != 0 ||
-      mq_launch_clear_state(dec->p.st, dec->p.x, s) != 0 ||
+      mq_launch_clear_state(dec->p.st, dec->p.x, s) != 0 || clear_fused_tags(dec, s) != 0 ||
       (dec->pf.cnt != nullptr && mq_launch_zero(dec->pf.cnt, dec->pf.cnt_bytes, s) != 0))
     return fail(MQ_ERR_HIP, "reset kernels failed to launch");
   dec->pos = 0;
@@ -465,11 +475,23 @@ int mq_prefill_fused(mq_decoder* dec, const int32_t* d_tokens, int n, const void
   f.patch_len = d_embeds != nullptr ? embeds_len : 0;
   f.tok_out = d_token_out;
   f.logits = d_logits;
+  // a tag that no row < n holds from an earlier launch (rows hold at most the three tags; when
+  // all three are present, the buffers are zeroed first)
+  unsigned used = 0;
+  for (int r = 0; r < n; ++r) used |= 1u << dec->fused_tag[r];
+  int tag = 1;
+  while (tag <= 3 && (used >> tag & 1u)) ++tag;
+  if (tag > 3) {
+    if (clear_fused_tags(dec, s) != 0) return fail(MQ_ERR_HIP, "fused buffer clear failed");
+    tag = 1;
+  }
+  f.tag = tag;
   const int rc = mq_launch_prefill_fused(dec->p, f, dec->grid, s);
   if (rc == -2 || rc == -3)
     return fail(MQ_ERR_UNSUPPORTED, "the fused prefill needs 256 co-resident workgroups (%d)",
                 dec->grid);
   if (rc != 0) return fail(MQ_ERR_HIP, "fused prefill launch failed (%d)", rc);
+  memset(dec->fused_tag, tag, (size_t)n);
   if (mq_launch_set_position(dec->p.st, dec->p.x, n, s) != 0)
     return fail(MQ_ERR_HIP, "state update failed");
   dec->pos = n;

@@ -1944,21 +1944,21 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, 
 // cooperative launch runs every layer over all n <= 64 prompt positions with fp32 activations
 // (bf16 weights, bf16 K/V cache rows, no rounding of the residual stream), then the final norm
 // and the LM head of the last position.
-// Here 256 workgroups x 512 threads run five stages per layer, separated by grid barriers:
-//   q|k|v GEMM (input RMSNorm folded in) -> attention per (kv head, 16-query block): q/k RMSNorm,
+// Here 256 workgroups x 512 threads run five stages per layer:
+//   q|k|v GEMM (input RMSNorm folded in) -> attention per (kv head, 4-query block): q/k RMSNorm,
 //   RoPE, K/V cache rows, causal softmax -> O GEMM + residual -> gate|up GEMM (post RMSNorm
 //   folded in) + silu(g) * u -> down GEMM + residual.
-// A GEMM stage's weight tiles (16 rows each) are loaded before the barrier that precedes the
-// stage, and its fp32 input rows with plain loads after it (every activation buffer of a launch is
-// written once and read only after the barrier that follows its writes).  The q|k|v and gate|up
-// stages give a workgroup one 16-row block and 1-4 column tiles (more as n grows, so that each
-// workgroup reads one block of input rows, staged straight into LDS); the O and down stages give
-// it one column tile and a quarter of the rows.  Products run on v_mfma_f32_16x16x32_bf16 with
+// There is no grid barrier.  The activations that cross XCDs (the residual stream, the attention
+// output, silu(g) * u) are tagged words (below) that each reader polls; q|k|v stays on the XCD
+// that computes it and is handed to its attention through an XCD-local barrier.  A GEMM stage
+// loads its weight tiles (16 rows each) first, then polls its fp32 input rows, which stream in
+// behind the tiles.  The q|k|v and gate|up stages give a workgroup one 16-row block and 1-4
+// column tiles (more as n grows, so that each workgroup reads one block of input rows, staged
+// straight into LDS); the O and down stages give it one column tile and a group of rows.  Products run on v_mfma_f32_16x16x32_bf16 with
 // the fp32 input split into three bf16 parts (hi + mid + lo represent it exactly), so each
 // product is the exact product of the fp32 value and the bf16 weight, accumulated in fp32.
 // The RMSNorm of a GEMM input is folded in: the MFMAs take x * w_norm and the epilogue scales
 // each row by rsqrt(mean(x^2) + eps), which the same pass accumulates.
-#define FP_STRIPES 32                    // barrier counter stripes, one 128-byte line each
 #define FPA_S 132                        // padded row stride (floats) of the attention tiles
 #define FP_IN_FLOATS (MQ_WAVES * (MQ_H / 256) * 2 * 256)   // the staged input block (K = H)
 #define FP_PART_FLOATS (8 * 4 * 256)                      // fp_gemm's partials
@@ -1969,57 +1969,18 @@ static_assert(FP_LDS_FLOATS >= 3 * 72 * FPA_KS / 2 + 64 * FPA_S + 2 * 8 * 64,
               "the attention carve fits");
 static_assert(FP_LDS_FLOATS >= MQ_LDS_FLOATS, "the LM head's LDS layout fits");
 
-// Grid barrier over the launch: every thread's stores complete before the workgroup arrives at
-// one of 32 counter stripes; lanes 0-31 of wave 0 poll all stripes until their sum reaches
-// `target` (the stripes start at zero, cleared by the launcher; counts stay far below 2^24, so
-// the float sum is exact).  Loads after the barrier are issued after the poll returns.
-// LOADS: vector loads this thread issued after its last store (the next stage's weight tile,
-// fp_tile_load); vmcnt counts loads and stores together and in issue order, so waiting for
-// vmcnt <= LOADS completes the stores while the weights stay in flight.
-template <int LOADS = 0>
-MQ_DEV void fp_grid_sync(uint32_t* bar, uint32_t target, MqSync* sy) {
-  static_assert(LOADS >= 0 && LOADS < 64, "vmcnt range");
-  // s_waitcnt vmcnt(LOADS) expcnt(7) lgkmcnt(15): only the vector memory counter
-  __builtin_amdgcn_s_waitcnt((LOADS & 15) | ((LOADS >> 4) << 14) | (7 << 4) | (15 << 8));
-  __syncthreads();
-  if (wave_id() == 0) {
-    const int lane = lane_id();
-    if (lane == 0)
-      __hip_atomic_fetch_add(bar + (blockIdx.x % FP_STRIPES) * 32, 1u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t spins = 0;
-    while (true) {
-      uint32_t v = 0;
-      if (lane < FP_STRIPES)
-        v = __hip_atomic_load(bar + lane * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (wave_sum((float)v) >= (float)target) break;
-      uint32_t ev = 0;
-      if (lane == 0 && (spins & 15) == 15)
-        ev = __hip_atomic_load(&sy->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (__builtin_amdgcn_readlane(ev, 0) != 0) break;
-      if (++spins > MQ_SPIN_LIMIT) {
-        if (lane == 0)
-          __hip_atomic_store(&sy->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-  }
-  __syncthreads();
-}
-
-// The launch's synchronization area (zeroed by the launcher): the grid barrier's 32 counter
-// stripes, then one role-claim counter per XCD, then per XCD one 128-byte line of flag words
-// (one per workgroup of the XCD) for the XCD-local barrier.
-#define FP_SYNC_WORDS ((FP_STRIPES + 2 * MQ_GROUPS) * 32)
-MQ_DEV uint32_t* fp_claims(uint32_t* bar) { return bar + FP_STRIPES * 32; }
-MQ_DEV uint32_t* fp_xflags(uint32_t* bar, int x) { return bar + (FP_STRIPES + MQ_GROUPS + x) * 32; }
+// The launch's synchronization area (zeroed by the launcher): one role-claim counter per XCD,
+// then per XCD one 128-byte line of flag words (one per workgroup of the XCD) for the XCD-local
+// barrier, each in its own 128-byte line.
+#define FP_SYNC_WORDS (2 * MQ_GROUPS * 32)
+MQ_DEV uint32_t* fp_claims(uint32_t* bar) { return bar; }
+MQ_DEV uint32_t* fp_xflags(uint32_t* bar, int x) { return bar + (MQ_GROUPS + x) * 32; }
 
 // Barrier of the workgroups of one XCD: each posts `e` in its flag word with a plain store (it
 // lands in the XCD's L2, where the others' sc1 loads find it) once its stores have completed,
 // and wave 0 polls the XCD's nw (<= 32) flags until every one is >= e (flags only grow within a
-// launch).  The error flag (every 16th round) or the spin bound ends the wait early, as in
-// fp_grid_sync.
+// launch).  The error flag (every 16th round) or the spin bound (which sets it) ends the wait
+// early.
 MQ_DEV void fp_xcd_sync(uint32_t* flags, int c, int nw, uint32_t e, MqSync* sy) {
   wait_all_memory();
   __syncthreads();
@@ -2047,6 +2008,64 @@ MQ_DEV void fp_xcd_sync(uint32_t* flags, int c, int nw, uint32_t e, MqSync* sy) 
   __syncthreads();
 }
 
+// Tagged activation words.  Every fp32 activation that crosses workgroups between the fused
+// prefill's stages (the residual stream, the attention output and silu(g) * u) is stored with
+// its two lowest mantissa bits replaced by the launch's tag (1, 2 or 3; the host picks one that
+// no row of the launch holds from an earlier launch, and cleared buffers hold 0), with a device-
+// scope store.  A reader polls its input words with device-scope loads until every one carries
+// the tag, so the data and its arrival are one round trip and no grid barrier is needed; it
+// removes the tag before use (a truncation below 2^-22 relative).  Each buffer is written once
+// per launch (per layer and stage), so a word with the tag is the launch's final value.
+MQ_DEV float fp_tagged(float v, uint32_t tag) {
+  return __uint_as_float((__float_as_uint(v) & ~3u) | tag);
+}
+MQ_DEV float fp_untag(float v) { return __uint_as_float(__float_as_uint(v) & ~3u); }
+MQ_DEV bool fp_tag4(uint4 u, uint32_t tag) {
+  return ((u.x & 3u) == tag) & ((u.y & 3u) == tag) & ((u.z & 3u) == tag) & ((u.w & 3u) == tag);
+}
+MQ_DEV void fp_st_tag(float* p, float v, uint32_t tag) { st_coh(p, fp_tagged(v, tag)); }
+// 16 bytes at byte offset `off` of the buffer from `base` (wave-uniform), with a device-scope
+// (sc1) buffer load: coherent across the XCDs' L2s like the agent-scope atomics, but an ordinary
+// load to the compiler (two 8-byte atomic loads per chunk made it spill the fused kernel's
+// registers)
+MQ_DEV uint4 fp_ld16_coh(const float* base, uint32_t off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7ffffff0, 0x00020000);
+  const mq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 16);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+// End of one round of a wave's poll: true once every lane's words carry the tag (`ok`), or when
+// a set error flag (read every 16th round) or the spin bound (which sets it) ends the wait.
+MQ_DEV bool fp_poll_done(bool ok, uint32_t& spins, MqSync* sy) {
+  if (__all(ok)) return true;
+  uint32_t ev = 0;
+  if (lane_id() == 0 && (spins & 15) == 15)
+    ev = __hip_atomic_load(&sy->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (__builtin_amdgcn_readlane(ev, 0) != 0) return true;
+  if (++spins > MQ_SPIN_LIMIT) {
+    if (lane_id() == 0)
+      __hip_atomic_store(&sy->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  }
+  __builtin_amdgcn_s_sleep(1);
+  return false;
+}
+// One tagged word, polled by this thread alone; returned without its tag.
+MQ_DEV float fp_poll1(const float* p, uint32_t tag, MqSync* sy) {
+  float v = ld_coh(p);
+  for (uint32_t spins = 0; (__float_as_uint(v) & 3u) != tag; v = ld_coh(p)) {
+    if ((spins & 15) == 15 &&
+        __hip_atomic_load(&sy->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
+      break;
+    if (++spins > MQ_SPIN_LIMIT) {
+      __hip_atomic_store(&sy->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return fp_untag(v);
+}
+
 // 16 weight rows (row0 .. row0 + 15, K bf16 each) as the B operand of the tile's MFMAs: wave w
 // holds the 32-wide k-steps w, w + 8, ...; lane l holds row l % 16, k-dims 8 (l / 16) .. + 8.
 template <int K>
@@ -2057,7 +2076,7 @@ struct FpTile {
 // loads, so that its L2 serves them after the first); otherwise non-temporal.
 template <int K>
 MQ_DEV void fp_tile_load(FpTile<K>& t, const bf16_t* row0, bool shared = false) {
-  // after every store of the stage (fp_grid_sync counts these loads as the last ones issued)
+  // after every store of the stage
   asm volatile("" ::: "memory");
   const int lane = lane_id(), wave = wave_id();
   const bf16_t* r = row0 + (size_t)(lane & 15) * K + 8 * (lane >> 4);
@@ -2110,13 +2129,13 @@ MQ_DEV void split3_bf16(const float (&x)[8], mq_bf16x8_t& hi, mq_bf16x8_t& mid, 
 
 // One residual GEMM tile (the O and down stages): C[r][c] = sum_k A[r][k] W[c][k] for the rows
 // row_lo <= r < n of 16-row blocks rb0 .. rb0 + nbr - 1 (nbr <= 4) of the fp32 input A (row
-// stride K; a buffer written once per launch, read with plain loads) and the 16 weight rows whose
+// stride K; tagged words, polled until every one carries `tag`) and the 16 weight rows whose
 // k-step j operand of this lane is tb(j) (FpTile order), then epi(row, col, v, res) for every
 // such row and the tile's 16 columns, where res = pre(row, col) is loaded before the products
 // (the residual), so its round trip overlaps them.  All 512 threads take part.
 template <int K, class TB, class Pre, class Epi>
 MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, TB tb, float* lds, Pre pre, Epi epi,
-                    int row_lo) {
+                    int row_lo, uint32_t tag, MqSync* sy) {
   // rows below row_lo are left to another workgroup (zero inputs, no outputs); block row i of
   // block b is row 16 (rb0 + b) + i
   const int lane = lane_id(), wave = wave_id();
@@ -2138,12 +2157,28 @@ MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, TB tb, float* lds, 
     uint4 u[K / 256][2];
     const int row = 16 * (rb0 + bb) + (lane & 15);
     const bool in = row >= row_lo && row < n;
+    // (rows outside [row_lo, n) load nothing and are zero)
+    const uint32_t src = 4u * (uint32_t)(row * K + 8 * (lane >> 4) + 32 * wave);
+    for (uint32_t spins = 0;;) {
+      bool ok = true;
+      if (in) {
 #pragma unroll
-    for (int j = 0; j < K / 256; ++j) {
-      const float* src = A + (size_t)row * K + 32 * (wave + 8 * j) + 8 * (lane >> 4);
-      u[j][0] = in ? ld16(src) : make_uint4(0, 0, 0, 0);
-      u[j][1] = in ? ld16(src + 4) : make_uint4(0, 0, 0, 0);
+        for (int j = 0; j < K / 256; ++j) {
+          u[j][0] = fp_ld16_coh(A, src + 4u * 256u * j);
+          u[j][1] = fp_ld16_coh(A, src + 4u * (256u * j + 4u));
+          ok &= fp_tag4(u[j][0], tag);
+          ok &= fp_tag4(u[j][1], tag);
+        }
+      }
+      if (fp_poll_done(ok, spins, sy)) break;
     }
+#pragma unroll
+    for (int j = 0; j < K / 256; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        u[j][h] = in ? make_uint4(u[j][h].x & ~3u, u[j][h].y & ~3u, u[j][h].z & ~3u,
+                                  u[j][h].w & ~3u)
+                     : make_uint4(0, 0, 0, 0);
     // the weight operands are fetched four k-steps at a time (from LDS they would otherwise be
     // read one k-step at a time, each read's latency in series with the products; all at once
     // would take 48 more registers)
@@ -2201,7 +2236,8 @@ MQ_DEV void fp_gemm(const float* A, int n, int rb0, int nbr, TB tb, float* lds, 
 // and the sums run in the same order as fp_gemm's.
 template <int K, int NG, int SUB, class Epi>
 MQ_DEV void fp_gemm_rows16(const float* A, int n, int rb, const bf16_t* w_norm,
-                           const FpTile<K> (&t)[NG * SUB], int ng, float* lds, Epi epi) {
+                           const FpTile<K> (&t)[NG * SUB], int ng, float* lds, Epi epi,
+                           uint32_t tag, MqSync* sy) {
   constexpr int NT = NG * SUB, KS = K / 256;
   static_assert(MQ_WAVES * KS * 2 * 256 <= FP_IN_FLOATS, "the staged input fits");
   const int lane = lane_id(), wave = wave_id();
@@ -2215,16 +2251,27 @@ MQ_DEV void fp_gemm_rows16(const float* A, int n, int rb, const bf16_t* w_norm,
   const int row = 16 * rb + (lane & 15);
   const bool in = row < n;
   const float* src = A + (size_t)min(row, n - 1) * K + 32 * wave + 8 * (lane >> 4);
-#pragma unroll
-  for (int j = 0; j < KS; ++j)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(src + 256 * j + 4 * h),
-          (__attribute__((address_space(3))) void*)(inp + (2 * j + h) * 256), 16, 0, 0);
   uint4 wn16[KS];
 #pragma unroll
   for (int j = 0; j < KS; ++j) wn16[j] = ld16(w_norm + 32 * (wave + 8 * j) + 8 * (lane >> 4));
+  // the wave's k-steps of the block, staged by device-scope (sc1) LDS loads and polled until
+  // every word carries the tag
+  for (uint32_t spins = 0;;) {
+#pragma unroll
+    for (int j = 0; j < KS; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(src + 256 * j + 4 * h),
+            (__attribute__((address_space(3))) void*)(inp + (2 * j + h) * 256), 16, 0, 16);
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < KS; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        ok &= fp_tag4(reinterpret_cast<const uint4*>(inp + (2 * j + h) * 256)[lane], tag);
+    if (fp_poll_done(ok, spins, sy)) break;
+  }
   mq_f32x4_t c[NT];
 #pragma unroll
   for (int q = 0; q < NT; ++q) c[q] = mq_f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -2233,7 +2280,8 @@ MQ_DEV void fp_gemm_rows16(const float* A, int n, int rb, const bf16_t* w_norm,
   for (int j = 0; j < KS; ++j) {
     const float4 a0 = reinterpret_cast<const float4*>(inp + 2 * j * 256)[lane];
     const float4 a1 = reinterpret_cast<const float4*>(inp + (2 * j + 1) * 256)[lane];
-    float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    float x[8] = {fp_untag(a0.x), fp_untag(a0.y), fp_untag(a0.z), fp_untag(a0.w),
+                  fp_untag(a1.x), fp_untag(a1.y), fp_untag(a1.z), fp_untag(a1.w)};
     if (!in)
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] = 0.f;
@@ -2484,7 +2532,8 @@ MQ_DEV void fp_attention(const MqDecodeParams& p, const MqFusedArgs& f, const Mq
     }
     st_coh64(reinterpret_cast<uint64_t*>(att + (size_t)pi * MQ_QDIM + (2 * h + (r & 1)) * MQ_D) +
                  lane,
-             (uint64_t)__float_as_uint(o0 * inv) | ((uint64_t)__float_as_uint(o1 * inv) << 32));
+             (uint64_t)__float_as_uint(fp_tagged(o0 * inv, (uint32_t)f.tag)) |
+                 ((uint64_t)__float_as_uint(fp_tagged(o1 * inv, (uint32_t)f.tag)) << 32));
   }
   __syncthreads();
 }
@@ -2513,16 +2562,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
     if (t == 0) __hip_atomic_store(&sy->err.v, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  uint32_t nbar = 0;
-  // LOADS: the weight-tile loads issued since the stage's last store, when `loaded`
-  auto grid_sync = [&](auto loads, bool loaded) {
-    constexpr int L = decltype(loads)::value;
-    if (loaded)
-      fp_grid_sync<L>(f.bar, (uint32_t)G * ++nbar, sy);
-    else
-      fp_grid_sync<0>(f.bar, (uint32_t)G * ++nbar, sy);
-  };
-  using std::integral_constant;
+  const uint32_t tag = (uint32_t)f.tag;
   constexpr int QKV = MQ_QDIM + 2 * MQ_KVDIM;
   // this launch's buffers: each written once, by one stage, and read after the next barrier
   auto hbuf = [&](int i) { return f.h + (size_t)i * MQ_FUSED_MAX_N * MQ_H; };
@@ -2543,16 +2583,18 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
     const bf16_t* src = patched ? f.patch + (size_t)pr * MQ_H : p.embed + (size_t)tok * MQ_H;
     const uint32_t v = ld32(src + 2 * t);
     st_coh64(reinterpret_cast<uint64_t*>(hbuf(0) + (size_t)row * MQ_H) + t,
-             (uint64_t)__float_as_uint(bf16_lo(v)) | ((uint64_t)__float_as_uint(bf16_hi(v)) << 32));
+             (uint64_t)__float_as_uint(fp_tagged(bf16_lo(v), tag)) |
+                 ((uint64_t)__float_as_uint(fp_tagged(bf16_hi(v), tag)) << 32));
   }
   const int nb = (n + 15) >> 4;
-  // The O and down stages have 1024 / 16 = 64 column tiles, each shared by four workgroups
-  // wg = tile + 64 part that take row groups of R = ceil(n / 4) rows (in the one or two 16-row
-  // MFMA blocks that hold them; the other block rows are zero), so every workgroup reads only its
-  // rows of the input.  The four of a tile run on one XCD (wg % 8 = tile % 8) and share its
-  // weights through the L2.
+  // The O and down stages have 1024 / 16 = 64 column tiles, each shared by up to four
+  // workgroups wg = tile + 64 part that take row groups of R rows, R the smallest of 1, 2, 4, 8,
+  // 16 that is >= n / 4, so that a group never straddles two 16-row MFMA blocks (the block's
+  // other rows are zero) and every workgroup reads only its rows of the input.  The workgroups
+  // of a tile run on one XCD (wg % 8 = tile % 8) and share its weights through the L2.
   const int hb_tile = wg % (MQ_H / 16), hb_part = wg / (MQ_H / 16);
-  const int hb_rows = (n + 3) / 4;
+  const int hb_q = (n + 3) / 4;
+  const int hb_rows = hb_q <= 1 ? 1 : hb_q <= 2 ? 2 : hb_q <= 4 ? 4 : hb_q <= 8 ? 8 : 16;
   const int hb_lo = hb_part * hb_rows, hb_hi = min(n, hb_lo + hb_rows), hb_rb = hb_lo / 16;
   const int hb_nb = hb_hi > hb_lo ? (hb_hi - 1) / 16 - hb_rb + 1 : 0;
   const bool hb_work = hb_lo < n;
@@ -2574,11 +2616,12 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
   };
   const int g_grp = wg % g_groups, g_rb = wg / g_groups;
   const bool q_tile = q_rb < nb, g_tile = g_rb < nb;
-  // Each GEMM stage loads its weight tiles, then waits at the grid barrier (whose poll is issued
-  // behind them: the tiles stream in while it waits), then runs; the three sit in one branch so
-  // that the tiles' registers never cross a join (the register allocator spills them otherwise).
+  // Each GEMM stage loads its weight tiles, then polls its tagged input rows (the polls are
+  // issued behind the tiles, which stream in meanwhile), then runs; the three sit in one branch
+  // so that the tiles' registers never cross a join (the register allocator spills them
+  // otherwise).  No grid barrier: every stage waits only for the words it reads.
   for (int l = 0; l < p.num_layers; ++l) {
-    const MqLayerW w = p.layers[l];
+    const MqLayerW* wl = p.layers + l;   // (fields read where used: fewer scalar registers held)
     const float* hin = hbuf(2 * l);
     float* hmid = hbuf(2 * l + 1);
     float* hout = hbuf(2 * l + 2);
@@ -2594,38 +2637,27 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
       FpTile<MQ_H> tq[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        if (q < qn) fp_tile_load(tq[q], qkv_row(w, 16 * qkv_tile(hx, q_grp * qn + q)), nb > 1);
-      if (qn == 1)
-        grid_sync(integral_constant<int, MQ_H / 256>(), true);
-      else if (qn == 2)
-        grid_sync(integral_constant<int, 2 * MQ_H / 256>(), true);
-      else
-        grid_sync(integral_constant<int, 4 * MQ_H / 256>(), true);
-      // (plain stores: only this XCD reads them)
-      fp_gemm_rows16<MQ_H, 4, 1>(hin, n, q_rb, w.in_ln, tq, qn, lds,
+        if (q < qn) fp_tile_load(tq[q], qkv_row(*wl, 16 * qkv_tile(hx, q_grp * qn + q)), nb > 1);
+      // (plain stores: only this XCD reads them, after the XCD barrier)
+      fp_gemm_rows16<MQ_H, 4, 1>(hin, n, q_rb, wl->in_ln, tq, qn, lds,
                                  [&](int row, int g, int col, const float* v) {
         qkvl[(size_t)row * QKV + 16 * qkv_tile(hx, q_grp * qn + g) + col] = v[0];
-      });
-    } else {
-      grid_sync(integral_constant<int, 0>(), false);
+      }, tag, sy);
     }
     // q|k|v -> attention inside each XCD; attention item (kv head xc, query block xj)
     fp_xcd_sync(fp_xflags(f.bar, xc), xj, NX, (uint32_t)(l + 1), sy);
-    if (xj < (n + FP_QB - 1) / FP_QB) fp_attention(p, f, w, l, xc, xj, qkvl, attl, lds);
+    if (xj < (n + FP_QB - 1) / FP_QB) fp_attention(p, f, *wl, l, xc, xj, qkvl, attl, lds);
     // O projection + residual (prefill_mk_o_proj_residual, :417-472)
     if (hb_work) {
       FpTile<MQ_QDIM> to;
-      fp_tile_load(to, w.wo + (size_t)16 * hb_tile * MQ_QDIM, hb_shared);
-      grid_sync(integral_constant<int, MQ_QDIM / 256>(), true);
+      fp_tile_load(to, wl->wo + (size_t)16 * hb_tile * MQ_QDIM, hb_shared);
       fp_gemm<MQ_QDIM>(attl, hb_hi, hb_rb, hb_nb, [&](int j) { return to.b[j]; }, lds,
                        [&](int row, int col) {
-                         return *gptr<float>(hin + (size_t)row * MQ_H + 16 * hb_tile + col);
+                         return fp_poll1(hin + (size_t)row * MQ_H + 16 * hb_tile + col, tag, sy);
                        },
                        [&](int row, int col, float v, float res) {
-        st_coh(hmid + (size_t)row * MQ_H + 16 * hb_tile + col, res + v);
-      }, hb_lo);
-    } else {
-      grid_sync(integral_constant<int, 0>(), false);
+        fp_st_tag(hmid + (size_t)row * MQ_H + 16 * hb_tile + col, res + v, tag);
+      }, hb_lo, tag, sy);
     }
     // post RMSNorm + gate|up + silu(g) * u (prefill_mk_mlp_gate_up, :474-544)
     if (g_tile) {
@@ -2633,52 +2665,40 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
       FpTile<MQ_H> tgu[6];
 #pragma unroll
       for (int q = 0; q < 3; ++q)
-        if (q < gp) fp_tile_load(tgu[q], w.wg + (size_t)16 * (g_grp * gp + q) * MQ_H, nb > 1);
+        if (q < gp) fp_tile_load(tgu[q], wl->wg + (size_t)16 * (g_grp * gp + q) * MQ_H, nb > 1);
 #pragma unroll
       for (int q = 0; q < 3; ++q)
-        if (q < gp) fp_tile_load(tgu[3 + q], w.wu + (size_t)16 * (g_grp * gp + q) * MQ_H, nb > 1);
-      if (gp == 1)
-        grid_sync(integral_constant<int, 2 * MQ_H / 256>(), true);
-      else if (gp == 2)
-        grid_sync(integral_constant<int, 4 * MQ_H / 256>(), true);
-      else
-        grid_sync(integral_constant<int, 6 * MQ_H / 256>(), true);
-      fp_gemm_rows16<MQ_H, 3, 2>(hmid, n, g_rb, w.post_ln, tgu, gp, lds,
+        if (q < gp) fp_tile_load(tgu[3 + q], wl->wu + (size_t)16 * (g_grp * gp + q) * MQ_H, nb > 1);
+      fp_gemm_rows16<MQ_H, 3, 2>(hmid, n, g_rb, wl->post_ln, tgu, gp, lds,
                                  [&](int row, int g, int col, const float* v) {
         const float gt = v[0], u = v[1];
-        st_coh(ml + (size_t)row * MQ_I + 16 * (g_grp * gp + g) + col, gt / (1.0f + expf(-gt)) * u);
-      });
-    } else {
-      grid_sync(integral_constant<int, 0>(), false);
+        fp_st_tag(ml + (size_t)row * MQ_I + 16 * (g_grp * gp + g) + col,
+                  gt / (1.0f + expf(-gt)) * u, tag);
+      }, tag, sy);
     }
     // down projection + residual (prefill_mk_mlp_down_residual, :546-599)
     if (hb_work) {
       // the tile in LDS (the stage's input rows take 96 registers)
       uint4* td = reinterpret_cast<uint4*>(lds + FP_PART_FLOATS);
-      fp_tile_load_lds<MQ_I>(td, w.wd + (size_t)16 * hb_tile * MQ_I);
-      grid_sync(integral_constant<int, MQ_I / 256>(), true);
-      // the tile has landed (its loads precede the barrier's poll); waiting here, before the
-      // input loads, lets the products start as the first input k-steps arrive instead of after
-      // the last (a read of LDS written by global_load_lds otherwise waits for every load)
-      wait_all_memory();
+      fp_tile_load_lds<MQ_I>(td, wl->wd + (size_t)16 * hb_tile * MQ_I);
+      // (the tile's LDS reads wait for every load, the input polls included)
       const uint4* tdw = td + wave_id() * (MQ_I / 256) * 64 + lane_id();
       fp_gemm<MQ_I>(ml, hb_hi, hb_rb, hb_nb, [&](int j) { return tdw[j * 64]; }, lds,
                     [&](int row, int col) {
-                      return *gptr<float>(hmid + (size_t)row * MQ_H + 16 * hb_tile + col);
+                      return fp_poll1(hmid + (size_t)row * MQ_H + 16 * hb_tile + col, tag, sy);
                     },
                     [&](int row, int col, float v, float res) {
-        st_coh(hout + (size_t)row * MQ_H + 16 * hb_tile + col, res + v);
-      }, hb_lo);
-    } else {
-      grid_sync(integral_constant<int, 0>(), false);
+        fp_st_tag(hout + (size_t)row * MQ_H + 16 * hb_tile + col, res + v, tag);
+      }, hb_lo, tag, sy);
     }
   }
-  // the last layer's residual stream (or the embeddings) is complete
-  grid_sync(integral_constant<int, 0>(), false);
-  // final RMSNorm of the last position (fp32, prefill_mk_final_norm, :601-650) + LM head argmax
-  const float2 hv = ldf2(hbuf(2 * p.num_layers) + (size_t)(n - 1) * MQ_H + 2 * t);
-  lds[LDS_IN + 2 * t] = hv.x;
-  lds[LDS_IN + 2 * t + 1] = hv.y;
+  // final RMSNorm of the last position (fp32, prefill_mk_final_norm, :601-650) + LM head argmax,
+  // from the last layer's residual stream (or the embeddings), polled
+  {
+    const float* hl = hbuf(2 * p.num_layers) + (size_t)(n - 1) * MQ_H;
+    lds[LDS_IN + 2 * t] = fp_poll1(hl + 2 * t, tag, sy);
+    lds[LDS_IN + 2 * t + 1] = fp_poll1(hl + 2 * t + 1, tag, sy);
+  }
   __syncthreads();
   lm_head_run(p, wg, G, lds, f.tok_out, f.logits, n - 1, false, false);
 }
@@ -2748,11 +2768,13 @@ static int launch_status() {
   return e == hipSuccess ? 0 : -(int)e - 1000;
 }
 
-size_t mq_fused_workspace_bytes(int num_layers) {
+size_t mq_fused_activation_bytes(int num_layers) {
   const size_t L = (size_t)(num_layers > 0 ? num_layers : 0);
   return (size_t)MQ_FUSED_MAX_N * 4 *
-             ((2 * L + 1) * MQ_H + L * (MQ_QDIM + 2 * MQ_KVDIM + MQ_QDIM + MQ_I)) +
-         FP_SYNC_WORDS * 4;
+         ((2 * L + 1) * MQ_H + L * (MQ_QDIM + 2 * MQ_KVDIM + MQ_QDIM + MQ_I));
+}
+size_t mq_fused_workspace_bytes(int num_layers) {
+  return mq_fused_activation_bytes(num_layers) + FP_SYNC_WORDS * 4;
 }
 void mq_fused_bind(MqFusedArgs* f, char* base, int num_layers) {
   const size_t L = (size_t)(num_layers > 0 ? num_layers : 0);
@@ -2777,7 +2799,7 @@ int mq_launch_prefill_fused(const MqDecodeParams& p, const MqFusedArgs& f, int g
   }
   if (!g_coop_ok || g_fused_blocks_per_cu < 1 || grid > g_cu_count * g_fused_blocks_per_cu)
     return -2;
-  if (grid < 256 || f.n < 1 || f.n > MQ_FUSED_MAX_N) return -3;
+  if (grid < 256 || f.n < 1 || f.n > MQ_FUSED_MAX_N || f.tag < 1 || f.tag > 3) return -3;
   if (grid / MQ_GROUPS > 32) return -3;   // fp_xcd_sync polls at most 32 flags per XCD
   const int rc = mq_launch_zero(f.bar, FP_SYNC_WORDS * 4, stream);
   if (rc != 0) return rc;

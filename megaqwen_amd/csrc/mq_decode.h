@@ -164,12 +164,10 @@ int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t st
 
 // Fused short-prompt prefill (mq_prefill_fused_kernel): fp32 buffers for up to
 // MQ_FUSED_MAX_N positions, in the decoder workspace (mq_fused_workspace_bytes).  Every
-// activation of a launch has a buffer of its own (one per layer and stage), written once and
-// read only after the barrier that follows its writes (a grid barrier; for q|k|v, which one XCD
-// both writes and reads, that XCD's barrier): no cache can then hold a stale copy of a line a
-// reader loads (caches start a kernel clean, and no line is read before it is written), so
-// readers use plain loads, served by their XCD's L2 after its first miss, instead of
-// device-coherent loads that each go to memory.
+// activation of a launch has a buffer of its own (one per layer and stage), written once.  h, att
+// and m cross XCDs as tagged words (the launch's tag in the two lowest mantissa bits, device-scope
+// stores), polled by their readers with device-scope loads; q|k|v, which one XCD both writes and
+// reads, is written with plain stores and read after that XCD's barrier.
 #define MQ_FUSED_MAX_N 64
 struct MqFusedArgs {
   float* h;                    // [2 L + 1][MQ_FUSED_MAX_N][H] residual stream: the embeddings,
@@ -178,9 +176,8 @@ struct MqFusedArgs {
   float* qkv;                  // [L][MQ_FUSED_MAX_N][4096] raw q | k | v projections
   float* att;                  // [L][MQ_FUSED_MAX_N][2048] attention output
   float* m;                    // [L][MQ_FUSED_MAX_N][I] silu(gate) * up
-  uint32_t* bar;               // sync area, zeroed per launch: grid-barrier counter stripes
-                               // (32 x 128 bytes), per-XCD role-claim counters and per-XCD
-                               // barrier flag lines (8 + 8 lines of 128 bytes)
+  uint32_t* bar;               // sync area, zeroed per launch: per-XCD role-claim counters and
+                               // per-XCD barrier flag lines (8 + 8 lines of 128 bytes)
   const int32_t* tokens;       // device token ids [n]
   int n;
   const bf16_t* patch;         // optional bf16 rows replacing the embeddings [patch_start, +len)
@@ -188,8 +185,13 @@ struct MqFusedArgs {
   int patch_len;
   int* tok_out;                // greedy next token
   float* logits;               // optional fp32 [vocab] of the last position
+  int tag;                     // 1..3: the tag of this launch's activation words in h, att and m
+                               // (no row < n of those buffers holds it from an earlier launch)
 };
 size_t mq_fused_workspace_bytes(int num_layers);
+// Bytes of the tagged activation buffers (h, qkv, att, m: one region from f.h), which must hold
+// zeros (no tag) before the first launch.
+size_t mq_fused_activation_bytes(int num_layers);
 void mq_fused_bind(MqFusedArgs* f, char* base, int num_layers);
 // One cooperative launch over `grid` (>= 256) workgroups; 1 <= f.n <= MQ_FUSED_MAX_N.
 int mq_launch_prefill_fused(const MqDecodeParams& p, const MqFusedArgs& f, int grid,

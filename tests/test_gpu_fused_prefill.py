@@ -99,6 +99,33 @@ def test_fused_prefill_deterministic(small):
     assert torch.equal(out[0][2], out[1][2]) and torch.equal(out[0][3], out[1][3])
 
 
+def test_fused_prefill_tags_across_launches(small):
+    """The fused prefill hands activations between workgroups as words tagged with the launch's
+    tag (1..3), which the host picks so that no row the launch reads still holds it from an
+    earlier launch; when rows hold all three tags, the buffers are cleared first.  Prompts of 64,
+    32 and 16 tokens leave all three tags in rows 0..63, so the next 64-token prompt takes the
+    clearing path; the others reuse rows last written one, two or more launches back.  With no
+    reset in between, every launch must give exactly the result of the same prompt after a reset
+    (token, logits and its K/V cache rows, bit for bit: the tag bits are removed before use)."""
+    dec, _, _, _ = small
+    lens = [64, 32, 16, 64, 7, 64, 1, 48, 33, 33, 16, 64]
+    prompts = {n: make_tokens(n, dec.vocab_size, seed=100 + n) for n in set(lens)}
+    ref = {}
+    for n, toks in prompts.items():
+        dec.reset()
+        tok, lg = dec.prefill_step_with_logits(toks)
+        ref[n] = (tok, lg.clone(), dec.k_cache[:, :, :n].clone(), dec.v_cache[:, :, :n].clone())
+    dec.reset()
+    for i, n in enumerate(lens):
+        tok, lg = dec.prefill_step_with_logits(prompts[n])
+        rtok, rlg, rk, rv = ref[n]
+        assert tok == rtok, (i, n)
+        assert torch.equal(lg, rlg), (i, n)
+        assert torch.equal(dec.k_cache[:, :, :n], rk) and torch.equal(dec.v_cache[:, :, :n], rv), (i, n)
+        assert dec.position() == n
+    dec.check()
+
+
 def test_fused_prefill_errors(small):
     dec, _, _, _ = small
     with pytest.raises(RuntimeError, match="Empty input sequence"):
