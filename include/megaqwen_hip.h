@@ -36,12 +36,13 @@ extern "C" {
 #define MQ_ERR_INVALID_ARG -1     /* null pointer, bad size, unsupported shape */
 #define MQ_ERR_HIP -2             /* a HIP runtime call failed */
 #define MQ_ERR_POSITION -3        /* position would exceed max_seq_len */
-#define MQ_ERR_DEVICE -4          /* the kernel reported an error (barrier time-out, bad input) */
+#define MQ_ERR_DEVICE -4          /* the kernel reported an error (wait time-out, bad input) */
 #define MQ_ERR_UNSUPPORTED -5     /* e.g. cooperative launch not available for persistent mode */
 
 /* Decode kernel organisation. */
-#define MQ_MODE_PERSISTENT 0      /* one cooperative kernel per token, grid barriers between phases */
-#define MQ_MODE_MULTI_KERNEL 1    /* one kernel launch per phase (no grid barriers) */
+#define MQ_MODE_PERSISTENT 0      /* one cooperative kernel per token (or chain of tokens); its phases
+                                     hand values over as epoch- or tag-carrying words */
+#define MQ_MODE_MULTI_KERNEL 1    /* one kernel launch per phase (launch boundaries order them) */
 
 /* One layer's bf16 weights (row-major, contiguous), same order and meaning as the reference's
  * LDGLayerWeights (fused_decode_ldg_common.inl:97-109) and its 11-per-layer flat list
@@ -149,9 +150,9 @@ int mq_debug_decode_step_layers(mq_decoder* dec, const int32_t* d_token_in,
 int mq_debug_decode_step_timing(mq_decoder* dec, const int32_t* d_token_in,
                                 int32_t* d_token_out, uint64_t* d_stamps, void* stream);
 
-/* Synchronises `stream` and returns MQ_ERR_DEVICE if a kernel flagged an error (barrier time-out,
- * bad position or token id).  The flag stays set until mq_decoder_reset; while it is set the
- * decode kernels skip their barrier waits, so results are not meaningful. */
+/* Synchronises `stream` and returns MQ_ERR_DEVICE if a kernel flagged an error (a wait that hit
+ * its spin limit, bad position or token id).  The flag stays set until mq_decoder_reset; while it
+ * is set the kernels end their waits early, so results are not meaningful. */
 int mq_decoder_check(mq_decoder* dec, void* stream);
 
 /* Exchange epochs of the persistent decode kernel.  No counterpart in the reference, whose
