@@ -1948,9 +1948,9 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_op_lm_kernel(MqDecodeParams p, 
 //   q|k|v GEMM (input RMSNorm folded in) -> attention per (kv head, 4-query block): q/k RMSNorm,
 //   RoPE, K/V cache rows, causal softmax -> O GEMM + residual -> gate|up GEMM (post RMSNorm
 //   folded in) + silu(g) * u -> down GEMM + residual.
-// There is no grid barrier.  The activations that cross XCDs (the residual stream, the attention
-// output, silu(g) * u) are tagged words (below) that each reader polls; q|k|v stays on the XCD
-// that computes it and is handed to its attention through an XCD-local barrier.  A GEMM stage
+// There is no barrier.  The activations that cross workgroups (the residual stream, q|k|v, the
+// attention output, silu(g) * u) are tagged words (below) that each reader polls; q|k|v stays on
+// the XCD that computes it, whose L2 serves its attention items.  A GEMM stage
 // loads its weight tiles (16 rows each) first, then polls its fp32 input rows, which stream in
 // behind the tiles.  The q|k|v and gate|up stages give a workgroup one 16-row block and 1-4
 // column tiles (more as n grows, so that each workgroup reads one block of input rows, staged
@@ -1970,52 +1970,19 @@ static_assert(FP_LDS_FLOATS >= 3 * 72 * FPA_KS / 2 + 64 * FPA_S + 2 * 8 * 64,
 static_assert(FP_LDS_FLOATS >= MQ_LDS_FLOATS, "the LM head's LDS layout fits");
 
 // The launch's synchronization area (zeroed by the launcher): one role-claim counter per XCD,
-// then per XCD one 128-byte line of flag words (one per workgroup of the XCD) for the XCD-local
-// barrier, each in its own 128-byte line.
-#define FP_SYNC_WORDS (2 * MQ_GROUPS * 32)
+// each in its own 128-byte line.
+#define FP_SYNC_WORDS (MQ_GROUPS * 32)
 MQ_DEV uint32_t* fp_claims(uint32_t* bar) { return bar; }
-MQ_DEV uint32_t* fp_xflags(uint32_t* bar, int x) { return bar + (MQ_GROUPS + x) * 32; }
-
-// Barrier of the workgroups of one XCD: each posts `e` in its flag word with a plain store (it
-// lands in the XCD's L2, where the others' sc1 loads find it) once its stores have completed,
-// and wave 0 polls the XCD's nw (<= 32) flags until every one is >= e (flags only grow within a
-// launch).  The error flag (every 16th round) or the spin bound (which sets it) ends the wait
-// early.
-MQ_DEV void fp_xcd_sync(uint32_t* flags, int c, int nw, uint32_t e, MqSync* sy) {
-  wait_all_memory();
-  __syncthreads();
-  if (wave_id() == 0) {
-    const int lane = lane_id();
-    if (lane == 0) st_local32(flags + c, e);
-    uint32_t spins = 0;
-    while (true) {
-      const uint32_t v = lane < nw ? __hip_atomic_load(flags + lane, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT)
-                                   : e;
-      if (__all(v >= e)) break;
-      uint32_t ev = 0;
-      if (lane == 0 && (spins & 15) == 15)
-        ev = __hip_atomic_load(&sy->err.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (__builtin_amdgcn_readlane(ev, 0) != 0) break;
-      if (++spins > MQ_SPIN_LIMIT) {
-        if (lane == 0)
-          __hip_atomic_store(&sy->err.v, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-  }
-  __syncthreads();
-}
 
 // Tagged activation words.  Every fp32 activation that crosses workgroups between the fused
-// prefill's stages (the residual stream, the attention output and silu(g) * u) is stored with
-// its two lowest mantissa bits replaced by the launch's tag (1, 2 or 3; the host picks one that
-// no row of the launch holds from an earlier launch, and cleared buffers hold 0), with a device-
-// scope store.  A reader polls its input words with device-scope loads until every one carries
-// the tag, so the data and its arrival are one round trip and no grid barrier is needed; it
-// removes the tag before use (a truncation below 2^-22 relative).  Each buffer is written once
-// per launch (per layer and stage), so a word with the tag is the launch's final value.
+// prefill's stages (the residual stream, q|k|v, the attention output and silu(g) * u) is stored
+// with its two lowest mantissa bits replaced by the launch's tag (1, 2 or 3; the host picks one
+// that no row of the launch holds from an earlier launch, and cleared buffers hold 0): with a
+// device-scope store, or for q|k|v, which only its own XCD reads, a plain store into that XCD's
+// L2.  A reader polls its input words with device-scope loads until every one carries the tag,
+// so the data and its arrival are one round trip and no barrier is needed; it removes the tag
+// before use (a truncation below 2^-22 relative).  Each buffer is written once per launch (per
+// layer and stage), so a word with the tag is the launch's final value.
 MQ_DEV float fp_tagged(float v, uint32_t tag) {
   return __uint_as_float((__float_as_uint(v) & ~3u) | tag);
 }
@@ -2033,6 +2000,13 @@ MQ_DEV uint4 fp_ld16_coh(const float* base, uint32_t off) {
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7ffffff0, 0x00020000);
   const mq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 16);
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+typedef unsigned int mq_u32x2 __attribute__((ext_vector_type(2)));
+MQ_DEV uint2 fp_ld8_coh(const float* base, uint32_t off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7ffffff0, 0x00020000);
+  const mq_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 16);
+  return make_uint2(v.x, v.y);
 }
 // End of one round of a wave's poll: true once every lane's words carry the tag (`ok`), or when
 // a set error flag (read every 16th round) or the spin bound (which sets it) ends the wait.
@@ -2416,9 +2390,10 @@ MQ_DEV void fp_attention(const MqDecodeParams& p, const MqFusedArgs& f, const Mq
   bf16_t* kc = p.kc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
   bf16_t* vc = p.vc + ((size_t)layer * MQ_NKV + h) * p.max_seq * MQ_D;
   // key rows in pairs, lanes 0-31 row j0 = wave + 16 i and lanes 32-63 row j0 + 8 (4 dims per
-  // lane, so a 16-byte load moves two rows), and this wave's query row: every load of the wave
-  // (raw rows and their RoPE table entries) is issued before the first is used, one round trip
-  // in all.  The second row of a pair past the keys loads row kn - 1 and is not stored.
+  // lane, so a 16-byte load moves two rows), and this wave's query row: the RoPE table entries,
+  // then the raw q|k|v words (tagged, written by this XCD), polled with device-scope loads until
+  // all carry the tag.  The second row of a pair past the keys loads row kn - 1 and is not
+  // stored.
   constexpr int KI = MQ_FUSED_MAX_N / (2 * MQ_WAVES);
   float4 kr[KI], vr[KI];
   uint2 kc4[KI], ks4[KI];
@@ -2431,17 +2406,38 @@ MQ_DEV void fp_attention(const MqDecodeParams& p, const MqFusedArgs& f, const Mq
     const int j0 = wave + 2 * MQ_WAVES * i;
     if (j0 < kn) {
       const int j = min(j0 + MQ_WAVES * half, kn - 1);
-      const float* row = qkv + (size_t)j * QKV;
-      kr[i] = ldf4(row + MQ_QDIM + h * MQ_D + m4);
-      vr[i] = ldf4(row + MQ_QDIM + MQ_KVDIM + h * MQ_D + m4);
       kc4[i] = ld8(p.cos + (size_t)j * MQ_D + m4);
       ks4[i] = ld8(p.sin + (size_t)j * MQ_D + m4);
     }
   }
   if (has_q) {
-    qr = ldf2(qkv + (size_t)pi * QKV + (2 * h + (r & 1)) * MQ_D + 2 * lane);
     qc2 = ld32(p.cos + (size_t)pi * MQ_D + 2 * lane);
     qs2 = ld32(p.sin + (size_t)pi * MQ_D + 2 * lane);
+  }
+  const uint32_t tag = (uint32_t)f.tag;
+  for (uint32_t spins = 0;;) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+      const int j0 = wave + 2 * MQ_WAVES * i;
+      if (j0 < kn) {
+        const int j = min(j0 + MQ_WAVES * half, kn - 1);
+        const uint32_t off = 4u * (uint32_t)(j * QKV + MQ_QDIM + h * MQ_D + m4);
+        const uint4 a = fp_ld16_coh(qkv, off), b = fp_ld16_coh(qkv, off + 4u * MQ_KVDIM);
+        ok &= fp_tag4(a, tag);
+        ok &= fp_tag4(b, tag);
+        kr[i] = make_float4(fp_untag(__uint_as_float(a.x)), fp_untag(__uint_as_float(a.y)),
+                            fp_untag(__uint_as_float(a.z)), fp_untag(__uint_as_float(a.w)));
+        vr[i] = make_float4(fp_untag(__uint_as_float(b.x)), fp_untag(__uint_as_float(b.y)),
+                            fp_untag(__uint_as_float(b.z)), fp_untag(__uint_as_float(b.w)));
+      }
+    }
+    if (has_q) {
+      const uint2 q = fp_ld8_coh(qkv, 4u * (uint32_t)(pi * QKV + (2 * h + (r & 1)) * MQ_D + 2 * lane));
+      ok &= ((q.x & 3u) == tag) & ((q.y & 3u) == tag);
+      qr = make_float2(fp_untag(__uint_as_float(q.x)), fp_untag(__uint_as_float(q.y)));
+    }
+    if (fp_poll_done(ok, spins, &p.st->sync)) break;
   }
 #pragma unroll
   for (int i = 0; i < KI; ++i) {
@@ -2638,14 +2634,13 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         if (q < qn) fp_tile_load(tq[q], qkv_row(*wl, 16 * qkv_tile(hx, q_grp * qn + q)), nb > 1);
-      // (plain stores: only this XCD reads them, after the XCD barrier)
+      // (tagged words with plain stores: only this XCD reads them, through its L2)
       fp_gemm_rows16<MQ_H, 4, 1>(hin, n, q_rb, wl->in_ln, tq, qn, lds,
                                  [&](int row, int g, int col, const float* v) {
-        qkvl[(size_t)row * QKV + 16 * qkv_tile(hx, q_grp * qn + g) + col] = v[0];
+        qkvl[(size_t)row * QKV + 16 * qkv_tile(hx, q_grp * qn + g) + col] = fp_tagged(v[0], tag);
       }, tag, sy);
     }
-    // q|k|v -> attention inside each XCD; attention item (kv head xc, query block xj)
-    fp_xcd_sync(fp_xflags(f.bar, xc), xj, NX, (uint32_t)(l + 1), sy);
+    // attention item (kv head xc, query block xj), from the q|k|v words of this XCD
     if (xj < (n + FP_QB - 1) / FP_QB) fp_attention(p, f, *wl, l, xc, xj, qkvl, attl, lds);
     // O projection + residual (prefill_mk_o_proj_residual, :417-472)
     if (hb_work) {
@@ -2800,7 +2795,7 @@ int mq_launch_prefill_fused(const MqDecodeParams& p, const MqFusedArgs& f, int g
   if (!g_coop_ok || g_fused_blocks_per_cu < 1 || grid > g_cu_count * g_fused_blocks_per_cu)
     return -2;
   if (grid < 256 || f.n < 1 || f.n > MQ_FUSED_MAX_N || f.tag < 1 || f.tag > 3) return -3;
-  if (grid / MQ_GROUPS > 32) return -3;   // fp_xcd_sync polls at most 32 flags per XCD
+  if (grid / MQ_GROUPS > 32) return -3;   // an XCD's 32 workgroups take the 32 q|k|v tiles of its head
   const int rc = mq_launch_zero(f.bar, FP_SYNC_WORDS * 4, stream);
   if (rc != 0) return rc;
   MqDecodeParams pc = p;

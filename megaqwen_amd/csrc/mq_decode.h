@@ -164,10 +164,10 @@ int mq_launch_decode(const MqDecodeParams& p, int mode, int grid, hipStream_t st
 
 // Fused short-prompt prefill (mq_prefill_fused_kernel): fp32 buffers for up to
 // MQ_FUSED_MAX_N positions, in the decoder workspace (mq_fused_workspace_bytes).  Every
-// activation of a launch has a buffer of its own (one per layer and stage), written once.  h, att
-// and m cross XCDs as tagged words (the launch's tag in the two lowest mantissa bits, device-scope
-// stores), polled by their readers with device-scope loads; q|k|v, which one XCD both writes and
-// reads, is written with plain stores and read after that XCD's barrier.
+// activation of a launch has a buffer of its own (one per layer and stage), written once, as
+// tagged words (the launch's tag in the two lowest mantissa bits) that their readers poll with
+// device-scope loads: h, att and m with device-scope stores (they cross XCDs), q|k|v, which one
+// XCD both writes and reads, with plain stores into that XCD's L2.
 #define MQ_FUSED_MAX_N 64
 struct MqFusedArgs {
   float* h;                    // [2 L + 1][MQ_FUSED_MAX_N][H] residual stream: the embeddings,
@@ -176,8 +176,8 @@ struct MqFusedArgs {
   float* qkv;                  // [L][MQ_FUSED_MAX_N][4096] raw q | k | v projections
   float* att;                  // [L][MQ_FUSED_MAX_N][2048] attention output
   float* m;                    // [L][MQ_FUSED_MAX_N][I] silu(gate) * up
-  uint32_t* bar;               // sync area, zeroed per launch: per-XCD role-claim counters and
-                               // per-XCD barrier flag lines (8 + 8 lines of 128 bytes)
+  uint32_t* bar;               // sync area, zeroed per launch: per-XCD role-claim counters (8
+                               // lines of 128 bytes)
   const int32_t* tokens;       // device token ids [n]
   int n;
   const bf16_t* patch;         // optional bf16 rows replacing the embeddings [patch_start, +len)
@@ -185,8 +185,8 @@ struct MqFusedArgs {
   int patch_len;
   int* tok_out;                // greedy next token
   float* logits;               // optional fp32 [vocab] of the last position
-  int tag;                     // 1..3: the tag of this launch's activation words in h, att and m
-                               // (no row < n of those buffers holds it from an earlier launch)
+  int tag;                     // 1..3: the tag of this launch's activation words (no row < n of
+                               // h, qkv, att or m holds it from an earlier launch)
 };
 size_t mq_fused_workspace_bytes(int num_layers);
 // Bytes of the tagged activation buffers (h, qkv, att, m: one region from f.h), which must hold
