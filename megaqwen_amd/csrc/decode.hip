@@ -2542,7 +2542,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
   // Role from the hardware placement, as the persistent decode kernel claims it: xc is the XCD
   // the workgroup runs on and xj the order of its claim there; the role index wg = xc + 8 xj
   // replaces the launch index everywhere, so wg % 8 is the XCD (the L2-shared tiles and the
-  // XCD-local q|k|v exchange rely on it).  A placement with more than G / 8 workgroups on one
+  // XCD-local q|k|v words rely on it).  A placement with more than G / 8 workgroups on one
   // XCD flags error 4; that workgroup returns and the others' waits end on the error flag.
   __shared__ int s_role;
   if (t == 0) {
@@ -2560,7 +2560,7 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
   }
   const uint32_t tag = (uint32_t)f.tag;
   constexpr int QKV = MQ_QDIM + 2 * MQ_KVDIM;
-  // this launch's buffers: each written once, by one stage, and read after the next barrier
+  // this launch's buffers: each written once, by one stage, as tagged words its readers poll
   auto hbuf = [&](int i) { return f.h + (size_t)i * MQ_FUSED_MAX_N * MQ_H; };
   auto qkvbuf = [&](int l) { return f.qkv + (size_t)l * MQ_FUSED_MAX_N * QKV; };
   auto attbuf = [&](int l) { return f.att + (size_t)l * MQ_FUSED_MAX_N * MQ_QDIM; };
@@ -2599,8 +2599,8 @@ __global__ void __launch_bounds__(MQ_THREADS) mq_prefill_fused_kernel(MqDecodePa
   // (gate|up: gp tiles of each), qn = 1, 2, 4, 4 and gp = 1, 2, 3, 3 for nb = 1 .. 4 row blocks,
   // and each reads one block of input rows, in one round trip.
   // q|k|v: XCD x computes the 32 tiles of kv head x (q heads 2x, 2x + 1, then k and v of x;
-  // tile i of the head is qkv_tile(i)), so that its attention reads them from its own L2 after
-  // an XCD-local barrier: member xj takes block xj / (32 / qn) and tiles qn (xj % (32 / qn)) + q.
+  // tile i of the head is qkv_tile(i)), so that its attention items poll them in its own L2:
+  // member xj takes block xj / (32 / qn) and tiles qn (xj % (32 / qn)) + q.
   // gate|up: wg = block * groups + group, so the nb workgroups of a column group run on one XCD
   // and share its weight tiles through the L2.
   const int qn = nb == 1 ? 1 : nb == 2 ? 2 : 4, gp = nb == 1 ? 1 : nb == 2 ? 2 : 3;
